@@ -1,0 +1,167 @@
+/*
+ * oxm.h -- C-ABI of the MI355X (gfx950) GEMM backend for oxmera.
+ *
+ * This is the boundary a Rust FFI crate (`oxmera-hip-sys`) binds; a safe
+ * `oxmera-hip` crate implements oxmera's `Backend` on top of it and registers
+ * it with the runtime.  Every entry point below names the reference interface
+ * it serves.  Plain pointers and sizes only; no exception or abort crosses it.
+ *
+ * Conventions
+ *  - Views follow oxmera's Layout (crates/oxmera-core/src/layout.rs:24-34):
+ *    shape, ELEMENT strides (signed: flipped views are representable,
+ *    layout.rs:6-10) and an element offset into the buffer at `data`.
+ *  - The caller owns every buffer.  Outputs are caller-allocated, contiguous,
+ *    sized by oxm_gemm_infer ("the output of every operation is a fresh
+ *    contiguous tensor on the operands' device", crates/oxmera-ops/src/lib.rs:16-17).
+ *  - Status codes map 1:1 onto oxmera_core::Error variants
+ *    (crates/oxmera-core/src/error.rs:14-102); oxm_last_error() returns a
+ *    thread-local message naming the operation and its operands.
+ *  - Validation runs completely before any device work is launched.
+ *  - stream == NULL: the call is synchronous (the result may be read as soon
+ *    as it returns, as MatmulOps::matmul returns a value).  A non-NULL
+ *    hipStream_t makes it asynchronous on that stream.
+ *  - Entry points are thread-safe (Backend: Send + Sync,
+ *    crates/oxmera-runtime/src/lib.rs:29).
+ */
+#ifndef OXM_H
+#define OXM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* oxmera_core::Error (error.rs:14-102), one code per variant, plus OXM_E_HIP
+ * for a HIP runtime failure and OXM_E_INVALID_ARGUMENT for a NULL or
+ * malformed argument at the ABI itself. */
+typedef enum {
+    OXM_OK = 0,
+    OXM_E_SHAPE_MISMATCH = 1,         /* Error::ShapeMismatch          error.rs:16-25 */
+    OXM_E_BROADCAST_INCOMPATIBLE = 2, /* Error::BroadcastIncompatible  error.rs:27-34 */
+    OXM_E_DTYPE_MISMATCH = 3,         /* Error::DTypeMismatch          error.rs:36-45 */
+    OXM_E_UNSUPPORTED_DTYPE = 4,      /* Error::UnsupportedDType       error.rs:47-54 */
+    OXM_E_DEVICE_MISMATCH = 5,        /* Error::DeviceMismatch         error.rs:56-65 */
+    OXM_E_INDEX_OUT_OF_BOUNDS = 6,    /* Error::IndexOutOfBounds       error.rs:67-74 */
+    OXM_E_RANK_MISMATCH = 7,          /* Error::RankMismatch           error.rs:76-83 */
+    OXM_E_BACKEND_UNAVAILABLE = 8,    /* Error::BackendUnavailable     error.rs:85-90 */
+    OXM_E_NOT_IMPLEMENTED = 9,        /* Error::NotImplemented         error.rs:92-101 */
+    OXM_E_HIP = 10,
+    OXM_E_INVALID_ARGUMENT = 11
+} oxm_status;
+
+/* oxmera_core::DType (dtype.rs:9-22) in declaration order, plus BF16 and F16,
+ * which this backend carries end to end (dtype.rs:5-6). */
+typedef enum {
+    OXM_F32 = 0,
+    OXM_F64 = 1,
+    OXM_I32 = 2,
+    OXM_I64 = 3,
+    OXM_U8 = 4,
+    OXM_BOOL = 5,
+    OXM_BF16 = 6,
+    OXM_F16 = 7
+} oxm_dtype;
+
+/* Epilogue activation applied in the GEMM's store stage. */
+typedef enum {
+    OXM_ACT_NONE = 0,  /* out = acc + bias                                   */
+    OXM_ACT_GELU = 1,  /* aux_out = acc + bias; out = GELU_erf(acc + bias)   */
+    OXM_ACT_DGELU = 2  /* out = acc * GELU_erf'(aux[m,n])  (backward of GELU) */
+} oxm_act;
+
+#define OXM_MAX_DIMS 8
+
+/* A strided view: oxmera_tensor::Tensor's Layout over its Storage
+ * (crates/oxmera-tensor/src/tensor.rs:15-19, layout.rs:24-34).
+ * device: -1 = host memory, >= 0 = HIP device index (Device, device.rs:10-24). */
+typedef struct {
+    void *data;
+    int32_t dtype;           /* oxm_dtype */
+    int32_t ndim;
+    const int64_t *shape;
+    const int64_t *strides;  /* elements, signed */
+    int64_t offset;          /* elements */
+    int32_t device;
+} oxm_view;
+
+/* Fused epilogue.  bias: [N] of bias_dtype on the device, or NULL.  aux: a
+ * contiguous [batch..., M, N] buffer of out_dtype: written with the
+ * pre-activation for OXM_ACT_GELU (may be NULL), read as Z for OXM_ACT_DGELU
+ * (required).  out_dtype must equal the dtype of the output view. */
+typedef struct {
+    const void *bias;
+    int32_t bias_dtype;
+    int32_t act;             /* oxm_act */
+    void *aux;
+} oxm_epilogue;
+
+/* Library version string. */
+const char *oxm_version(void);
+
+/* Thread-local description of the last failure on this thread: the operation
+ * and its operands (exercises/a5-error-taxonomy/tests/spec.rs:62-80). */
+const char *oxm_last_error(void);
+
+/* Number of HIP devices this backend can serve; OXM_E_BACKEND_UNAVAILABLE when
+ * the HIP runtime finds none (backend_for's typed refusal,
+ * crates/oxmera-runtime/src/lib.rs:36-44). */
+oxm_status oxm_device_count(int32_t *count);
+
+/* Backend::name() (crates/oxmera-runtime/src/lib.rs:33). */
+const char *oxm_backend_name(void);
+
+/* broadcast_shapes (crates/oxmera-core/src/shape.rs:45-58): NumPy rules; on
+ * refusal OXM_E_BROADCAST_INCOMPATIBLE and the message carries both operands
+ * verbatim (exercises/a2-broadcasting/tests/spec.rs:38-54). */
+oxm_status oxm_broadcast_shapes(int32_t lhs_ndim, const int64_t *lhs, int32_t rhs_ndim, const int64_t *rhs,
+                                int32_t *out_ndim, int64_t *out_shape);
+
+/* Shape rules of MatmulOps::matmul (crates/oxmera-ops/src/lib.rs:52-59),
+ * extended to rank >= 2 with NumPy batch broadcasting over the leading dims:
+ * [..., m, k] x [..., k, n] -> [broadcast(...), m, n].  Rank < 2 is
+ * OXM_E_RANK_MISMATCH, an inner-dim mismatch OXM_E_SHAPE_MISMATCH,
+ * differing dtypes OXM_E_DTYPE_MISMATCH.  out_shape holds OXM_MAX_DIMS. */
+oxm_status oxm_gemm_infer(const oxm_view *a, const oxm_view *b, int32_t *out_ndim, int64_t *out_shape);
+
+/* MatmulOps::matmul (crates/oxmera-ops/src/lib.rs:52-59; reference body
+ * CpuBackend::matmul, crates/oxmera-cpu/src/lib.rs:71-76), on the GPU:
+ * c = epilogue(a . b).  a, b: any strided views (transposed, sliced,
+ * broadcast batch dims) of F32, BF16 or F16 on one device; they are read in
+ * place, never copied.  c: contiguous view of the inferred shape, F32 for F32
+ * inputs, F32/BF16/F16 for 16-bit inputs (f32 accumulation throughout).
+ * ep may be NULL (plain matmul).  stream: hipStream_t or NULL. */
+oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, const oxm_epilogue *ep,
+                    void *stream);
+
+/* ReduceOps::sum over one axis of a rank-2 contiguous tensor
+ * (crates/oxmera-ops/src/lib.rs:61-69): out[c] = sum_r x[r, c] (axis 0) with
+ * f32 accumulation.  The bias gradient of oxmera-nn Linear.  x: F32/BF16/F16
+ * [R, C] contiguous view on the device; out: F32 [C] contiguous view. */
+oxm_status oxm_sum_rows(const oxm_view *x, const oxm_view *out, void *stream);
+
+/* Mean-squared-error loss and its gradient (the MLP's objective; composed in
+ * the reference from BinaryOps::sub/mul and ReduceOps::sum,
+ * crates/oxmera-ops/src/lib.rs:39-69): loss[0] = mean((y - t)^2) (f32, device),
+ * dy = 2 (y - t) / numel in dy's dtype.  y, t, dy: contiguous, same shape. */
+oxm_status oxm_mse_loss_grad(const oxm_view *y, const oxm_view *t, const oxm_view *loss, const oxm_view *dy,
+                             void *stream);
+
+/* Storage for device tensors (crates/oxmera-tensor/src/storage.rs:12-32,
+ * "GPU variants hold opaque backend handles", :19-24). */
+oxm_status oxm_alloc(int32_t device, size_t bytes, void **out);
+oxm_status oxm_free(int32_t device, void *ptr);
+
+/* Byte copy between host (-1) and device (>= 0) memory; synchronous when
+ * stream is NULL. */
+oxm_status oxm_copy(void *dst, int32_t dst_device, const void *src, int32_t src_device, size_t bytes, void *stream);
+
+/* Wait for all work on the device. */
+oxm_status oxm_synchronize(int32_t device);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OXM_H */

@@ -1,0 +1,69 @@
+"""Build the gfx950 backend library ``oxmera_amd/liboxm.so`` in-tree.
+
+Each HIP / C++ translation unit under ``oxmera_amd/csrc`` is compiled with
+``hipcc --offload-arch=gfx950`` into ``oxmera_amd/_build`` (in parallel),
+then linked into one shared library exporting the C-ABI of
+``include/oxm.h``.  hipcc cross-compiles, so this runs without a GPU.
+
+Usage: ``python -m oxmera_amd.build`` (or ``__graft_entry__.build()``).
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "liboxm.so"
+ARCH = os.environ.get("OXM_GFX", "gfx950")
+
+SOURCES = ["oxm_capi.cpp", "gemm.hip", "gemm_f32.hip", "gemm_bf16.hip", "gemm_f16.hip", "glue.hip"]
+
+# -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 on this pool.
+COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-Wno-unused-command-line-argument"]
+
+
+def _hipcc() -> str:
+    exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(exe).exists():
+        raise RuntimeError("hipcc not found: the gfx950 backend cannot be built")
+    return exe
+
+
+def _compile(src: str) -> Path:
+    obj = BUILD / (src.replace(".", "_") + ".o")
+    lang = ["-x", "hip"]
+    cmd = [_hipcc(), *COMMON, *lang, "-c", str(CSRC / src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    return obj
+
+
+def build(verbose: bool = True) -> Path:
+    """Compile every translation unit and link ``liboxm.so``; returns its path."""
+    BUILD.mkdir(exist_ok=True)
+    jobs = min(len(SOURCES), max(1, min(os.cpu_count() or 1, 16)))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, SOURCES))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [_hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}", flush=True)
+    return LIB
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

@@ -1,0 +1,32 @@
+// gemm.hip -- tile-shape table and dtype dispatch of the GEMM kernels.
+// The instantiations live in one translation unit per dtype
+// (gemm_f32.hip, gemm_bf16.hip, gemm_f16.hip) so they build in parallel.
+#include "gemm_launch.hpp"
+#include "gemm_kernels.hpp"
+
+namespace oxm {
+
+hipError_t launch_gemm_f32(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipStream_t s);
+hipError_t launch_gemm_bf16(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipStream_t s);
+hipError_t launch_gemm_f16(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipStream_t s);
+
+TileShape tile_shape(int cfg) {
+    switch (cfg) {
+    case kCfgH_256: return {256, 256};
+    case kCfgH_128: return {128, 128};
+    default: return {128, 128};
+    }
+}
+
+hipError_t launch_gemm(GemmArgs args, int dtype, int ld_a, int ld_b, int cfg, hipStream_t stream) {
+    TileShape ts = tile_shape(cfg);
+    args.tiles_m = (int32_t)((args.M + ts.bm - 1) / ts.bm);
+    args.tiles_n = (int32_t)((args.N + ts.bn - 1) / ts.bn);
+    args.group_m = 8;
+    args.xcd_remap = 1;
+    if (dtype == kDtF32) return launch_gemm_f32(args, ld_a, ld_b, cfg, stream);
+    if (dtype == kDtBF16) return launch_gemm_bf16(args, ld_a, ld_b, cfg, stream);
+    return launch_gemm_f16(args, ld_a, ld_b, cfg, stream);
+}
+
+}  // namespace oxm

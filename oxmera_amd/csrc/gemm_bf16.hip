@@ -1,0 +1,11 @@
+// gemm_bf16.hip -- bf16-input instantiations (v_mfma_f32_32x32x16_bf16).
+#include "gemm_dispatch.hpp"
+
+namespace oxm {
+
+hipError_t launch_gemm_bf16(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipStream_t s) {
+    if (cfg == kCfgH_256) return pick_a<bf16_t, 256, 256, 2, 2>(a, ld_a, ld_b, s);
+    return pick_a<bf16_t, 128, 128, 2, 2>(a, ld_a, ld_b, s);
+}
+
+}  // namespace oxm

@@ -1,0 +1,36 @@
+// gemm_dispatch.hpp -- maps runtime loader kinds onto kernel instantiations.
+#pragma once
+#include "gemm_kernels.hpp"
+#include "gemm_launch.hpp"
+
+namespace oxm {
+
+constexpr int kSwz = 0;  // LDS XOR pattern (see lds_off)
+
+template <typename T, int BM, int BN, int WM, int WN, Ld LA, Ld LB>
+hipError_t launch_one(const GemmArgs &a, hipStream_t s) {
+    int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n * a.batch;
+    dim3 grid((unsigned)ntiles), block(WM * WN * 64);
+    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WM, WN, LA, LB, kSwz>), grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
+template <typename T, int BM, int BN, int WM, int WN, Ld LA>
+hipError_t pick_b(const GemmArgs &a, int lb, hipStream_t s) {
+    switch (lb) {
+    case kLdK: return launch_one<T, BM, BN, WM, WN, LA, Ld::K>(a, s);
+    case kLdMN: return launch_one<T, BM, BN, WM, WN, LA, Ld::MN>(a, s);
+    default: return launch_one<T, BM, BN, WM, WN, LA, Ld::G>(a, s);
+    }
+}
+
+template <typename T, int BM, int BN, int WM, int WN>
+hipError_t pick_a(const GemmArgs &a, int la, int lb, hipStream_t s) {
+    switch (la) {
+    case kLdK: return pick_b<T, BM, BN, WM, WN, Ld::K>(a, lb, s);
+    case kLdMN: return pick_b<T, BM, BN, WM, WN, Ld::MN>(a, lb, s);
+    default: return pick_b<T, BM, BN, WM, WN, Ld::G>(a, lb, s);
+    }
+}
+
+}  // namespace oxm

@@ -1,0 +1,10 @@
+// gemm_f32.hip -- f32 instantiations (v_mfma_f32_32x32x2_f32).
+#include "gemm_dispatch.hpp"
+
+namespace oxm {
+
+hipError_t launch_gemm_f32(const GemmArgs &a, int ld_a, int ld_b, int /*cfg*/, hipStream_t s) {
+    return pick_a<float, 128, 128, 2, 2>(a, ld_a, ld_b, s);
+}
+
+}  // namespace oxm

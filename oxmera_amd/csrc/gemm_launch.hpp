@@ -1,0 +1,28 @@
+// gemm_launch.hpp -- host-side entry into the GEMM kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "gemm_args.hpp"
+
+namespace oxm {
+
+// Operand loader kinds (the kernel's Ld enum, as plain ints for the host).
+enum LoaderKind : int { kLdK = 0, kLdMN = 1, kLdG = 2 };
+
+// Tile configurations.
+enum TileCfg : int {
+    kCfgF32_128 = 0,   // f32: 128x128 tile, 2x2 waves of 64x64, BK 32
+    kCfgH_256 = 1,     // bf16/f16: 256x256 tile, 2x2 waves of 128x128, BK 64
+    kCfgH_128 = 2,     // bf16/f16: 128x128 tile, 2x2 waves of 64x64, BK 64
+};
+
+struct TileShape {
+    int bm, bn;
+};
+TileShape tile_shape(int cfg);
+
+// Launch one batched GEMM.  `args` must be fully validated by the caller;
+// tiles_m/tiles_n/group_m/xcd_remap are filled in here.
+hipError_t launch_gemm(GemmArgs args, int dtype, int ld_a, int ld_b, int cfg, hipStream_t stream);
+
+}  // namespace oxm

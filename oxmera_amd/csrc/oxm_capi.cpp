@@ -1,0 +1,496 @@
+// oxm_capi.cpp -- the C-ABI of the gfx950 GEMM backend (include/oxm.h).
+//
+// Host-side responsibilities: validate every argument (shapes, strides,
+// dtypes, devices, and that each view lies inside its device allocation) and
+// report failures as oxmera's typed errors; classify each operand's layout to
+// pick a global loader; fill the kernel argument block and launch.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "../../include/oxm.h"
+#include "gemm_args.hpp"
+#include "gemm_launch.hpp"
+#include "glue_launch.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+oxm_status fail(oxm_status st, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return st;
+}
+
+oxm_status ok() {
+    g_last_error.clear();
+    return OXM_OK;
+}
+
+// Debug-style rendering of a shape, "[2, 3]", as oxmera's Shape prints.
+std::string shape_str(int n, const int64_t *d) {
+    std::string s = "[";
+    for (int i = 0; i < n; ++i) {
+        if (i) s += ", ";
+        s += std::to_string((long long)d[i]);
+    }
+    return s + "]";
+}
+
+const char *dtype_name(int dt) {
+    switch (dt) {
+    case OXM_F32: return "F32";
+    case OXM_F64: return "F64";
+    case OXM_I32: return "I32";
+    case OXM_I64: return "I64";
+    case OXM_U8: return "U8";
+    case OXM_BOOL: return "Bool";
+    case OXM_BF16: return "BF16";
+    case OXM_F16: return "F16";
+    default: return "?";
+    }
+}
+
+int dtype_size(int dt) {
+    switch (dt) {
+    case OXM_F32: case OXM_I32: return 4;
+    case OXM_F64: case OXM_I64: return 8;
+    case OXM_U8: case OXM_BOOL: return 1;
+    case OXM_BF16: case OXM_F16: return 2;
+    default: return 0;
+    }
+}
+
+std::string device_str(int d) { return d < 0 ? std::string("Cpu") : "Rocm { index: " + std::to_string(d) + " }"; }
+
+bool is_gemm_dtype(int dt) { return dt == OXM_F32 || dt == OXM_BF16 || dt == OXM_F16; }
+
+// Structural checks of a view: pointers, rank, non-negative extents and offset.
+oxm_status check_view(const oxm_view *v, const char *what, const char *op) {
+    if (!v) return fail(OXM_E_INVALID_ARGUMENT, "%s: %s view is NULL", op, what);
+    if (v->ndim < 0 || v->ndim > OXM_MAX_DIMS)
+        return fail(OXM_E_RANK_MISMATCH, "%s: %s has rank %d, supported 0..%d", op, what, v->ndim, OXM_MAX_DIMS);
+    if (v->ndim > 0 && (!v->shape || !v->strides))
+        return fail(OXM_E_INVALID_ARGUMENT, "%s: %s has NULL shape or strides", op, what);
+    if (dtype_size(v->dtype) == 0) return fail(OXM_E_INVALID_ARGUMENT, "%s: %s has unknown dtype %d", op, what, v->dtype);
+    for (int i = 0; i < v->ndim; ++i)
+        if (v->shape[i] < 0) return fail(OXM_E_INVALID_ARGUMENT, "%s: %s has negative extent", op, what);
+    if (v->offset < 0) return fail(OXM_E_INVALID_ARGUMENT, "%s: %s has negative offset", op, what);
+    return OXM_OK;
+}
+
+int64_t numel(const oxm_view *v) {
+    int64_t n = 1;
+    for (int i = 0; i < v->ndim; ++i) n *= v->shape[i];
+    return n;
+}
+
+bool is_contiguous(const oxm_view *v) {
+    int64_t expect = 1;
+    for (int i = v->ndim - 1; i >= 0; --i) {
+        if (v->shape[i] != 1 && v->strides[i] != expect) return false;
+        expect *= v->shape[i];
+    }
+    return true;
+}
+
+// The device allocation holding [p, p + bytes) must contain it entirely and
+// live on `device`.  This is what keeps a malformed view from reaching the
+// GPU as an out-of-bounds access.
+oxm_status check_device_range(const void *p, int64_t lo_bytes, int64_t hi_bytes, int device, const char *what,
+                              const char *op) {
+    hipPointerAttribute_t attr;
+    memset(&attr, 0, sizeof attr);
+    hipError_t e = hipPointerGetAttributes(&attr, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(OXM_E_DEVICE_MISMATCH, "%s: %s (%p) is not HIP device memory", op, what, p);
+    }
+    if (attr.type != hipMemoryTypeDevice && attr.type != hipMemoryTypeManaged)
+        return fail(OXM_E_DEVICE_MISMATCH, "%s: %s (%p) is not device memory", op, what, p);
+    if (attr.device != device)
+        return fail(OXM_E_DEVICE_MISMATCH, "%s: %s lives on %s, expected %s", op, what, device_str(attr.device).c_str(),
+                    device_str(device).c_str());
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    e = hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(OXM_E_HIP, "%s: cannot query the allocation of %s", op, what);
+    }
+    const char *b = (const char *)base;
+    const char *lo = (const char *)p + lo_bytes;
+    const char *hi = (const char *)p + hi_bytes;
+    if (lo < b || hi > b + size)
+        return fail(OXM_E_INDEX_OUT_OF_BOUNDS,
+                    "%s: %s addresses bytes [%lld, %lld) relative to its pointer, outside its %zu-byte allocation", op,
+                    what, (long long)(lo - (const char *)p), (long long)(hi - (const char *)p), size);
+    return OXM_OK;
+}
+
+// Every byte a strided view can address must lie in its allocation
+// (Tensor::from_storage's rule, crates/oxmera-tensor/src/tensor.rs:21-28).
+oxm_status check_view_memory(const oxm_view *v, const char *what, const char *op) {
+    if (numel(v) == 0) return OXM_OK;
+    int es = dtype_size(v->dtype);
+    int64_t lo = v->offset, hi = v->offset;
+    for (int i = 0; i < v->ndim; ++i) {
+        int64_t span = (v->shape[i] - 1) * v->strides[i];
+        if (span < 0) lo += span;
+        else hi += span;
+    }
+    return check_device_range(v->data, lo * es, (hi + 1) * es, v->device, what, op);
+}
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+oxm_status hip_fail(hipError_t e, const char *op) {
+    return fail(OXM_E_HIP, "%s: HIP error %d (%s)", op, (int)e, hipGetErrorString(e));
+}
+
+oxm_status finish(hipStream_t s, const char *op) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, op);
+    if (!s) {
+        e = hipStreamSynchronize(nullptr);
+        if (e != hipSuccess) return hip_fail(e, op);
+    }
+    return ok();
+}
+
+// Operand loader choice from the view's strides (see gemm_kernels.hpp).
+int classify(const char *ptr, int64_t s_mn, int64_t s_k, int64_t mn, int64_t k, const int64_t *bstr, int nbd,
+             int es) {
+    const int64_t vec = 16 / es;
+    bool aligned = ((uintptr_t)ptr % 16) == 0;
+    bool batch_ok = true;
+    for (int d = 0; d < nbd; ++d) batch_ok = batch_ok && (bstr[d] % vec == 0);
+    if (mn == 1) s_mn = 0;
+    if (k == 1) s_k = 0;
+    if (aligned && batch_ok && s_k == 1 && k % vec == 0 && s_mn % vec == 0) return oxm::kLdK;
+    if (aligned && batch_ok && s_mn == 1 && mn % vec == 0 && s_k % vec == 0) return oxm::kLdMN;
+    return oxm::kLdG;
+}
+
+int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *oxm_version(void) { return "oxmera-mi355x 0.1.0 (gfx950)"; }
+
+const char *oxm_last_error(void) { return g_last_error.c_str(); }
+
+const char *oxm_backend_name(void) { return "hip-gfx950"; }
+
+oxm_status oxm_device_count(int32_t *count) {
+    if (!count) return fail(OXM_E_INVALID_ARGUMENT, "device_count: NULL out pointer");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        *count = 0;
+        return fail(OXM_E_BACKEND_UNAVAILABLE, "no backend available for device Rocm { index: 0 }: no HIP device");
+    }
+    *count = n;
+    return ok();
+}
+
+oxm_status oxm_broadcast_shapes(int32_t na, const int64_t *a, int32_t nb, const int64_t *b, int32_t *nout,
+                                int64_t *out) {
+    if (na < 0 || nb < 0 || na > OXM_MAX_DIMS || nb > OXM_MAX_DIMS || (na && !a) || (nb && !b) || !nout || !out)
+        return fail(OXM_E_INVALID_ARGUMENT, "broadcast_shapes: malformed arguments");
+    int n = na > nb ? na : nb;
+    int64_t tmp[OXM_MAX_DIMS];
+    for (int i = 0; i < n; ++i) {
+        int ia = na - n + i, ib = nb - n + i;
+        int64_t da = ia >= 0 ? a[ia] : 1, db = ib >= 0 ? b[ib] : 1;
+        if (da == db || db == 1)
+            tmp[i] = da;
+        else if (da == 1)
+            tmp[i] = db;
+        else
+            return fail(OXM_E_BROADCAST_INCOMPATIBLE, "cannot broadcast %s with %s", shape_str(na, a).c_str(),
+                        shape_str(nb, b).c_str());
+    }
+    for (int i = 0; i < n; ++i) out[i] = tmp[i];
+    *nout = n;
+    return ok();
+}
+
+oxm_status oxm_gemm_infer(const oxm_view *a, const oxm_view *b, int32_t *out_ndim, int64_t *out_shape) {
+    const char *op = "matmul";
+    oxm_status st;
+    if ((st = check_view(a, "lhs", op)) != OXM_OK) return st;
+    if ((st = check_view(b, "rhs", op)) != OXM_OK) return st;
+    if (!out_ndim || !out_shape) return fail(OXM_E_INVALID_ARGUMENT, "matmul: NULL output shape pointer");
+    if (a->ndim < 2 || b->ndim < 2)
+        return fail(OXM_E_RANK_MISMATCH, "rank mismatch in matmul: operands of rank %d and %d, both must be >= 2",
+                    a->ndim, b->ndim);
+    if (a->dtype != b->dtype)
+        return fail(OXM_E_DTYPE_MISMATCH, "dtype mismatch: expected %s, got %s in matmul", dtype_name(a->dtype),
+                    dtype_name(b->dtype));
+    const int64_t k = a->shape[a->ndim - 1];
+    if (b->shape[b->ndim - 2] != k) {
+        int64_t exp[OXM_MAX_DIMS];
+        for (int i = 0; i < b->ndim; ++i) exp[i] = b->shape[i];
+        exp[b->ndim - 2] = k;
+        return fail(OXM_E_SHAPE_MISMATCH, "shape mismatch: expected %s, got %s in matmul",
+                    shape_str(b->ndim, exp).c_str(), shape_str(b->ndim, b->shape).c_str());
+    }
+    int32_t nbd = 0;
+    int64_t bshape[OXM_MAX_DIMS];
+    st = oxm_broadcast_shapes(a->ndim - 2, a->shape, b->ndim - 2, b->shape, &nbd, bshape);
+    if (st != OXM_OK) return st;
+    for (int i = 0; i < nbd; ++i) out_shape[i] = bshape[i];
+    out_shape[nbd] = a->shape[a->ndim - 2];
+    out_shape[nbd + 1] = b->shape[b->ndim - 1];
+    *out_ndim = nbd + 2;
+    return ok();
+}
+
+oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, const oxm_epilogue *ep, void *stream) {
+    const char *op = "matmul";
+    int32_t nd = 0;
+    int64_t oshape[OXM_MAX_DIMS];
+    oxm_status st = oxm_gemm_infer(a, b, &nd, oshape);
+    if (st != OXM_OK) return st;
+    if ((st = check_view(c, "out", op)) != OXM_OK) return st;
+    if (!is_gemm_dtype(a->dtype))
+        return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by matmul", dtype_name(a->dtype));
+    if (a->dtype == OXM_F32 ? c->dtype != OXM_F32 : !is_gemm_dtype(c->dtype))
+        return fail(OXM_E_DTYPE_MISMATCH, "dtype mismatch: expected %s, got %s in matmul (output)",
+                    a->dtype == OXM_F32 ? "F32" : "F32/BF16/F16", dtype_name(c->dtype));
+    if (c->ndim != nd || memcmp(c->shape, oshape, sizeof(int64_t) * nd) != 0)
+        return fail(OXM_E_SHAPE_MISMATCH, "shape mismatch: expected %s, got %s in matmul (output)",
+                    shape_str(nd, oshape).c_str(), shape_str(c->ndim, c->shape).c_str());
+    if (!is_contiguous(c)) return fail(OXM_E_NOT_IMPLEMENTED, "matmul is not implemented for a non-contiguous output");
+    if (a->device < 0 || b->device != a->device || c->device != a->device)
+        return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s vs %s in matmul", device_str(a->device).c_str(),
+                    device_str(a->device != b->device ? b->device : c->device).c_str());
+    const int nbd = nd - 2;
+    if (nbd > oxm::kMaxBatchDims)
+        return fail(OXM_E_NOT_IMPLEMENTED, "matmul is not implemented for %d batch dims (max %d)", nbd,
+                    oxm::kMaxBatchDims);
+    oxm_epilogue none = {nullptr, OXM_F32, OXM_ACT_NONE, nullptr};
+    if (!ep) ep = &none;
+    if (ep->act < OXM_ACT_NONE || ep->act > OXM_ACT_DGELU)
+        return fail(OXM_E_INVALID_ARGUMENT, "matmul: unknown epilogue activation %d", ep->act);
+    if (ep->act == OXM_ACT_DGELU && !ep->aux)
+        return fail(OXM_E_INVALID_ARGUMENT, "matmul: the DGELU epilogue needs the pre-activation (aux)");
+    if (ep->bias && !is_gemm_dtype(ep->bias_dtype))
+        return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by matmul (bias)", dtype_name(ep->bias_dtype));
+
+    const int64_t M = oshape[nd - 2], N = oshape[nd - 1], K = a->shape[a->ndim - 1];
+    int64_t batch = 1;
+    for (int i = 0; i < nbd; ++i) batch *= oshape[i];
+    if (batch == 0 || M == 0 || N == 0) return ok();
+
+    DeviceGuard guard(a->device);
+    if ((st = check_view_memory(a, "lhs", op)) != OXM_OK) return st;
+    if ((st = check_view_memory(b, "rhs", op)) != OXM_OK) return st;
+    if ((st = check_view_memory(c, "out", op)) != OXM_OK) return st;
+    const int oes = dtype_size(c->dtype);
+    if (ep->bias && (st = check_device_range(ep->bias, 0, N * dtype_size(ep->bias_dtype), a->device, "bias", op)) !=
+                        OXM_OK)
+        return st;
+    if (ep->aux && (st = check_device_range(ep->aux, 0, batch * M * N * oes, a->device, "aux", op)) != OXM_OK)
+        return st;
+
+    const int es = dtype_size(a->dtype);
+    oxm::GemmArgs g;
+    memset(&g, 0, sizeof g);
+    g.a = (const char *)a->data + a->offset * es;
+    g.b = (const char *)b->data + b->offset * es;
+    g.c = (char *)c->data + c->offset * oes;
+    g.bias = ep->bias;
+    g.aux = ep->aux;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.sam = a->strides[a->ndim - 2];
+    g.sak = a->strides[a->ndim - 1];
+    g.sbk = b->strides[b->ndim - 2];
+    g.sbn = b->strides[b->ndim - 1];
+    g.nbd = nbd;
+    g.batch = batch;
+    for (int d = 0; d < nbd; ++d) {
+        int da = a->ndim - 2 - nbd + d, db = b->ndim - 2 - nbd + d;
+        g.bext[d] = oshape[d];
+        g.bsa[d] = (da >= 0 && a->shape[da] != 1) ? a->strides[da] : 0;
+        g.bsb[d] = (db >= 0 && b->shape[db] != 1) ? b->strides[db] : 0;
+    }
+    g.act = ep->act;
+    g.out_dtype = c->dtype;
+    g.bias_dtype = ep->bias_dtype;
+
+    int ld_a = classify((const char *)g.a, g.sam, g.sak, M, K, g.bsa, nbd, es);
+    int ld_b = classify((const char *)g.b, g.sbn, g.sbk, N, K, g.bsb, nbd, es);
+    int cfg;
+    if (a->dtype == OXM_F32) {
+        cfg = oxm::kCfgF32_128;
+    } else {
+        int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
+        cfg = big_tiles >= 256 ? oxm::kCfgH_256 : oxm::kCfgH_128;
+        cfg = env_int("OXM_GEMM_CFG", cfg);
+        if (cfg != oxm::kCfgH_256 && cfg != oxm::kCfgH_128) cfg = oxm::kCfgH_128;
+    }
+    oxm::TileShape ts = oxm::tile_shape(cfg);
+    int64_t ntiles = ((M + ts.bm - 1) / ts.bm) * ((N + ts.bn - 1) / ts.bn) * batch;
+    if (ntiles > 0x7fffffffLL) return fail(OXM_E_NOT_IMPLEMENTED, "matmul is not implemented for %lld tiles", (long long)ntiles);
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = oxm::launch_gemm(g, a->dtype, ld_a, ld_b, cfg, s);
+    if (e != hipSuccess) return hip_fail(e, op);
+    return finish(s, op);
+}
+
+oxm_status oxm_sum_rows(const oxm_view *x, const oxm_view *out, void *stream) {
+    const char *op = "sum";
+    oxm_status st;
+    if ((st = check_view(x, "input", op)) != OXM_OK) return st;
+    if ((st = check_view(out, "out", op)) != OXM_OK) return st;
+    if (x->ndim != 2) return fail(OXM_E_RANK_MISMATCH, "sum: input of rank %d, expected 2", x->ndim);
+    if (!is_gemm_dtype(x->dtype)) return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by sum", dtype_name(x->dtype));
+    if (out->dtype != OXM_F32) return fail(OXM_E_DTYPE_MISMATCH, "dtype mismatch: expected F32, got %s in sum", dtype_name(out->dtype));
+    if (out->ndim != 1 || out->shape[0] != x->shape[1])
+        return fail(OXM_E_SHAPE_MISMATCH, "shape mismatch: expected [%lld], got %s in sum", (long long)x->shape[1],
+                    shape_str(out->ndim, out->shape).c_str());
+    if (!is_contiguous(x) || !is_contiguous(out))
+        return fail(OXM_E_NOT_IMPLEMENTED, "sum is not implemented for non-contiguous views");
+    if (x->device < 0 || out->device != x->device)
+        return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s vs %s in sum", device_str(x->device).c_str(),
+                    device_str(out->device).c_str());
+    if (out->shape[0] == 0) return ok();
+    DeviceGuard guard(x->device);
+    if ((st = check_view_memory(x, "input", op)) != OXM_OK) return st;
+    if ((st = check_view_memory(out, "out", op)) != OXM_OK) return st;
+    int es = dtype_size(x->dtype);
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = oxm::launch_sum_rows((const char *)x->data + x->offset * es, x->dtype, x->shape[0], x->shape[1],
+                                        (float *)out->data + out->offset, s);
+    if (e != hipSuccess) return hip_fail(e, op);
+    return finish(s, op);
+}
+
+oxm_status oxm_mse_loss_grad(const oxm_view *y, const oxm_view *t, const oxm_view *loss, const oxm_view *dy,
+                             void *stream) {
+    const char *op = "mse_loss";
+    oxm_status st;
+    if ((st = check_view(y, "y", op)) != OXM_OK) return st;
+    if ((st = check_view(t, "target", op)) != OXM_OK) return st;
+    if ((st = check_view(loss, "loss", op)) != OXM_OK) return st;
+    if ((st = check_view(dy, "dy", op)) != OXM_OK) return st;
+    if (!is_gemm_dtype(y->dtype)) return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by mse_loss", dtype_name(y->dtype));
+    if (t->dtype != y->dtype || dy->dtype != y->dtype)
+        return fail(OXM_E_DTYPE_MISMATCH, "dtype mismatch: expected %s, got %s in mse_loss", dtype_name(y->dtype),
+                    dtype_name(t->dtype != y->dtype ? t->dtype : dy->dtype));
+    if (loss->dtype != OXM_F32 || numel(loss) != 1)
+        return fail(OXM_E_SHAPE_MISMATCH, "shape mismatch: mse_loss needs a one-element F32 loss");
+    if (t->ndim != y->ndim || dy->ndim != y->ndim || memcmp(t->shape, y->shape, 8 * y->ndim) ||
+        memcmp(dy->shape, y->shape, 8 * y->ndim))
+        return fail(OXM_E_SHAPE_MISMATCH, "shape mismatch: expected %s, got %s in mse_loss", shape_str(y->ndim, y->shape).c_str(),
+                    shape_str(t->ndim, t->shape).c_str());
+    if (!is_contiguous(y) || !is_contiguous(t) || !is_contiguous(dy))
+        return fail(OXM_E_NOT_IMPLEMENTED, "mse_loss is not implemented for non-contiguous views");
+    if (y->device < 0 || t->device != y->device || dy->device != y->device || loss->device != y->device)
+        return fail(OXM_E_DEVICE_MISMATCH, "device mismatch in mse_loss");
+    const int64_t n = numel(y);
+    if (n == 0) return fail(OXM_E_SHAPE_MISMATCH, "mse_loss of an empty tensor has no mean");
+    DeviceGuard guard(y->device);
+    if ((st = check_view_memory(y, "y", op)) != OXM_OK) return st;
+    if ((st = check_view_memory(t, "target", op)) != OXM_OK) return st;
+    if ((st = check_view_memory(dy, "dy", op)) != OXM_OK) return st;
+    if ((st = check_view_memory(loss, "loss", op)) != OXM_OK) return st;
+    int es = dtype_size(y->dtype);
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = oxm::launch_mse((const char *)y->data + y->offset * es, (const char *)t->data + t->offset * es,
+                                   (char *)dy->data + dy->offset * es, y->dtype, n, (float *)loss->data + loss->offset, s);
+    if (e != hipSuccess) return hip_fail(e, op);
+    return finish(s, op);
+}
+
+oxm_status oxm_alloc(int32_t device, size_t bytes, void **out) {
+    if (!out) return fail(OXM_E_INVALID_ARGUMENT, "alloc: NULL out pointer");
+    *out = nullptr;
+    if (device < 0) return fail(OXM_E_DEVICE_MISMATCH, "alloc: device %d is not a HIP device", device);
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device >= n) {
+        (void)hipGetLastError();
+        return fail(OXM_E_BACKEND_UNAVAILABLE, "no backend available for device %s", device_str(device).c_str());
+    }
+    DeviceGuard guard(device);
+    hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        *out = nullptr;
+        return hip_fail(e, "alloc");
+    }
+    return ok();
+}
+
+oxm_status oxm_free(int32_t device, void *ptr) {
+    if (!ptr) return ok();
+    DeviceGuard guard(device < 0 ? 0 : device);
+    hipError_t e = hipFree(ptr);
+    if (e != hipSuccess) return hip_fail(e, "free");
+    return ok();
+}
+
+oxm_status oxm_copy(void *dst, int32_t dst_device, const void *src, int32_t src_device, size_t bytes, void *stream) {
+    if (bytes == 0) return ok();
+    if (!dst || !src) return fail(OXM_E_INVALID_ARGUMENT, "copy: NULL pointer");
+    hipMemcpyKind kind;
+    if (dst_device < 0 && src_device < 0)
+        kind = hipMemcpyHostToHost;
+    else if (dst_device < 0)
+        kind = hipMemcpyDeviceToHost;
+    else if (src_device < 0)
+        kind = hipMemcpyHostToDevice;
+    else
+        kind = hipMemcpyDeviceToDevice;
+    if (dst_device >= 0) {
+        oxm_status st = check_device_range(dst, 0, (int64_t)bytes, dst_device, "dst", "copy");
+        if (st != OXM_OK) return st;
+    }
+    if (src_device >= 0) {
+        oxm_status st = check_device_range(src, 0, (int64_t)bytes, src_device, "src", "copy");
+        if (st != OXM_OK) return st;
+    }
+    DeviceGuard guard(dst_device >= 0 ? dst_device : (src_device >= 0 ? src_device : 0));
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = s ? hipMemcpyAsync(dst, src, bytes, kind, s) : hipMemcpy(dst, src, bytes, kind);
+    if (e != hipSuccess) return hip_fail(e, "copy");
+    return ok();
+}
+
+oxm_status oxm_synchronize(int32_t device) {
+    if (device < 0) return ok();
+    DeviceGuard guard(device);
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(e, "synchronize");
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,255 @@
+"""GPU parity of the gfx950 GEMM against the CPU oracle, through the C-ABI.
+
+Configurations from the north star (BASELINE.json "configs"):
+  C1  f32 256^3 contiguous, U[-1,1)                 -> checked in full
+  C2  f32 4096^3 N(0,1); odd 4097 x 4095 x 4093     -> sampled rows + full checksums
+  C3  bf16 8192^3, B a transposed view [1, 8192]    -> sampled rows + full checksums
+  C4  f32 batched: A every other row of [32,1024,1024], B [1,1024,768] broadcast
+                                                    -> sampled rows + per-batch checksums
+plus every operand layout the loaders distinguish (K-contiguous, M/N-contiguous,
+generic strided, negative strides, offsets) for f32/bf16/f16 at odd sizes in
+full, the A4 hand-computed cases, the fused epilogues, and the refusals that
+need device memory.  Tolerance (north star): |c-r| <= tol * max(|r|, rms(r)),
+tol = 1e-5*sqrt(K) for f32, 1e-2 for bf16/f16 inputs.
+"""
+import numpy as np
+import pytest
+
+import oxmera_amd as ox
+from oracle import oracle as O
+from tests.parity import (Operand, assert_close, checksum_residuals, contiguous_operand, host_buffer,
+                          sample_rows, spec_tolerance, to_f32)
+
+pytestmark = pytest.mark.gpu
+
+F32, BF16, F16 = ox.DType.F32, ox.DType.BF16, ox.DType.F16
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+# ---- A4 spec cases on the GPU (exact) -------------------------------------------
+
+def test_a4_hand_computed_cases(hip):
+    d = ox.Device.rocm(0)
+    t = lambda v, s: ox.Tensor.from_numpy(np.array(v, np.float32).reshape(s), d)
+    assert hip.matmul(t([1, 2, 3, 4], (2, 2)), t([5, 6, 7, 8], (2, 2))).to_numpy().tolist() == [[19, 22], [43, 50]]
+    assert hip.matmul(t([1, 2, 3, 4, 5, 6], (2, 3)), t([1, 10, 100], (3, 1))).to_numpy().tolist() == [[321], [654]]
+    a = [[1.5, -2.0], [0.25, 4.0]]
+    assert hip.matmul(t(a, (2, 2)), t([1, 0, 0, 1], (2, 2))).to_numpy().tolist() == a
+    assert hip.matmul(t([3, -1, 2, 7, .5, -4], (2, 3)), t([0] * 6, (3, 2))).to_numpy().tolist() == [[0, 0], [0, 0]]
+    bt = t([5, 7, 6, 8], (2, 2)).permute([1, 0])  # transposed view, never copied
+    assert hip.matmul(t([1, 2, 3, 4], (2, 2)), bt).to_numpy().tolist() == [[19, 22], [43, 50]]
+    # TensorOps route through the registry
+    assert t([1, 2, 3, 4], (2, 2)).matmul(t([5, 6, 7, 8], (2, 2))).to_numpy().tolist() == [[19, 22], [43, 50]]
+
+
+def test_a4_refusals_on_device(hip):
+    d = ox.Device.rocm(0)
+    with pytest.raises(ox.ShapeMismatch):
+        hip.matmul(ox.Tensor.empty((2, 3), F32, d), ox.Tensor.empty((4, 2), F32, d))
+    with pytest.raises(ox.RankMismatch):
+        hip.matmul(ox.Tensor.empty((6,), F32, d), ox.Tensor.empty((6,), F32, d))
+    with pytest.raises(ox.DTypeMismatch):
+        hip.matmul(ox.Tensor.empty((2, 3), F32, d), ox.Tensor.empty((3, 2), BF16, d))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_transpose_law_and_column_independence(hip, seed):
+    rng = np.random.default_rng(seed)
+    d = ox.Device.rocm(0)
+    a = ox.Tensor.from_numpy(rng.uniform(-8, 8, (2, 3)).astype(np.float32), d)
+    b = ox.Tensor.from_numpy(rng.uniform(-8, 8, (3, 2)).astype(np.float32), d)
+    x = hip.matmul(a, b).to_numpy().T
+    y = hip.matmul(b.permute([1, 0]), a.permute([1, 0])).to_numpy()
+    assert np.all(np.abs(x - y) <= 1e-4 * (1 + np.maximum(np.abs(x), np.abs(y))))
+    full = hip.matmul(a, b).to_numpy()
+    col = hip.matmul(a, b.narrow(1, seed % 2, 1)).to_numpy()
+    assert np.all(np.abs(full[:, seed % 2] - col[:, 0]) <= 1e-4 * (1 + np.abs(full[:, seed % 2])))
+
+
+# ---- every loader layout, full comparison at odd sizes ---------------------------
+
+def make_operand(dtype, kind, rows, cols, seed, which):
+    """An operand of logical shape [rows, cols] laid out per `kind`."""
+    rng = np.random.default_rng(seed)
+    if kind == "row":        # contiguous, last dim unit
+        buf = host_buffer(dtype, rng.uniform(-1, 1, rows * cols).astype(np.float32))
+        return Operand(dtype, buf, (rows, cols), (cols, 1), 0)
+    if kind == "col":        # transposed view: first dim unit
+        buf = host_buffer(dtype, rng.uniform(-1, 1, rows * cols).astype(np.float32))
+        return Operand(dtype, buf, (rows, cols), (1, rows), 0)
+    if kind == "gather":     # every other row of a bigger buffer, with an offset
+        buf = host_buffer(dtype, rng.uniform(-1, 1, 5 + 2 * rows * (cols + 3)).astype(np.float32))
+        return Operand(dtype, buf, (rows, cols), (2 * (cols + 3), 1), 5)
+    if kind == "flip":       # rows reversed (negative stride)
+        buf = host_buffer(dtype, rng.uniform(-1, 1, rows * cols).astype(np.float32))
+        return Operand(dtype, buf, (rows, cols), (-cols, 1), (rows - 1) * cols)
+    if kind == "colgap":     # column-major with a padded leading dim (MN-contiguous, aligned)
+        ld = rows + 8
+        buf = host_buffer(dtype, rng.uniform(-1, 1, ld * cols).astype(np.float32))
+        return Operand(dtype, buf, (rows, cols), (1, ld), 0)
+    raise ValueError(kind)
+
+
+LAYOUTS = ["row", "col", "gather", "flip", "colgap"]
+SHAPES = [(64, 128, 64), (70, 136, 90), (300, 64, 260), (33, 200, 17), (257, 96, 129)]
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, F16], ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("la", LAYOUTS)
+@pytest.mark.parametrize("lb", LAYOUTS)
+def test_layouts_full(hip, dtype, la, lb):
+    for si, (m, k, n) in enumerate(SHAPES):
+        a = make_operand(dtype, la, m, k, 1000 + si, "a")
+        b = make_operand(dtype, lb, k, n, 2000 + si, "b")
+        log(f"layouts {dtype.name} {la}x{lb} M={m} K={k} N={n}")
+        c = hip.matmul(a.dev, b.dev)
+        ref = O.matmul(a.ora, b.ora)
+        assert_close(to_f32(c), ref, spec_tolerance(dtype, k), f"{dtype.name} {la}x{lb} {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
+def test_batched_broadcast_small(hip, dtype):
+    rng = np.random.default_rng(3)
+    # A [3, 2, 37, 40] (every other row), B [2, 40, 45] -> [3, 2, 37, 45]
+    abuf = host_buffer(dtype, rng.uniform(-1, 1, 3 * 2 * 74 * 40).astype(np.float32))
+    a = Operand(dtype, abuf, (3, 2, 37, 40), (2 * 74 * 40, 74 * 40, 80, 1))
+    bbuf = host_buffer(dtype, rng.uniform(-1, 1, 2 * 40 * 45).astype(np.float32))
+    b = Operand(dtype, bbuf, (2, 40, 45), (1800, 45, 1))
+    c = hip.matmul(a.dev, b.dev)
+    assert c.shape == (3, 2, 37, 45)
+    assert_close(to_f32(c), O.matmul(a.ora, b.ora), spec_tolerance(dtype, 40), "batched")
+
+
+def test_zero_sized_and_k_zero(hip):
+    d = ox.Device.rocm(0)
+    c = hip.matmul(ox.Tensor.empty((0, 5), F32, d), ox.Tensor.empty((5, 3), F32, d))
+    assert c.shape == (0, 3)
+    a = ox.Tensor.empty((4, 0), F32, d)
+    b = ox.Tensor.empty((0, 6), F32, d)
+    assert np.array_equal(hip.matmul(a, b).to_numpy(), np.zeros((4, 6), np.float32))
+
+
+# ---- epilogues --------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype,out", [(F32, F32), (BF16, F32), (BF16, BF16), (F16, F16)],
+                         ids=["f32", "bf16-f32", "bf16-bf16", "f16-f16"])
+def test_bias_gelu_epilogue(hip, dtype, out):
+    rng = np.random.default_rng(21)
+    m, k, n = 130, 192, 200
+    a = contiguous_operand(dtype, rng.normal(0, 1, (m, k)))
+    b = make_operand(dtype, "col", k, n, 22, "b")
+    bias_vals = rng.normal(0, 0.5, n).astype(np.float32)
+    bias_buf = host_buffer(dtype, bias_vals)
+    bias = ox.Tensor.from_numpy(bias_buf, ox.Device.rocm(0), dtype)
+    z = ox.Tensor.empty((m, n), out, ox.Device.rocm(0))
+    c = hip.matmul(a.dev, b.dev, out_dtype=out, bias=bias, act=ox.ACT_GELU, aux=z)
+    odt = {F32: O.F32, BF16: O.BF16, F16: O.F16}[out]
+    ref, ref_z = O.matmul(a.ora, b.ora, out_dtype=odt, bias=bias_buf, bias_dtype={F32: O.F32, BF16: O.BF16,
+                                                                                   F16: O.F16}[dtype],
+                          act=O.ACT_GELU, want_aux=True)
+    widen = (lambda x: O.bf16_to_f32(x)) if out == BF16 else ((lambda x: x.view(np.float16).astype(np.float32))
+                                                              if out == F16 else (lambda x: x))
+    tol = spec_tolerance(dtype, k) if out == F32 else 1e-2
+    assert_close(to_f32(z), widen(ref_z), tol, "pre-activation")
+    assert_close(to_f32(c), widen(ref), tol, "gelu output")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
+def test_dgelu_epilogue(hip, dtype):
+    rng = np.random.default_rng(31)
+    m, k, n = 96, 160, 130
+    a = contiguous_operand(dtype, rng.normal(0, 1, (m, k)))
+    b = make_operand(dtype, "col", k, n, 32, "b")
+    zvals = rng.normal(0, 1, (m, n)).astype(np.float32)
+    zbuf = host_buffer(dtype, zvals.reshape(-1)).reshape(m, n)
+    z = ox.Tensor.from_numpy(zbuf, ox.Device.rocm(0), dtype)
+    c = hip.matmul(a.dev, b.dev, out_dtype=dtype, act=ox.ACT_DGELU, aux=z)
+    odt = O.F32 if dtype == F32 else O.BF16
+    ref = O.matmul(a.ora, b.ora, out_dtype=odt, act=O.ACT_DGELU, aux=zbuf)
+    refw = ref if dtype == F32 else O.bf16_to_f32(ref)
+    assert_close(to_f32(c), refw, spec_tolerance(dtype, k), "dgelu")
+
+
+# ---- refusals that need device memory ------------------------------------------------
+
+def test_view_outside_allocation_is_refused(hip):
+    d = ox.Device.rocm(0)
+    base = ox.Tensor.empty((64,), F32, d)
+    # a [8, 8] view with stride 9 addresses 8*9 - 1 + 1 = 72 > 64 elements
+    bad = ox.Tensor(base.storage, ox.Layout((8, 8), (9, 1), 0))
+    with pytest.raises(ox.IndexOutOfBounds):
+        hip.matmul(bad, ox.Tensor.empty((8, 8), F32, d))
+
+
+def test_dgelu_requires_aux(hip):
+    d = ox.Device.rocm(0)
+    with pytest.raises(ox.InvalidArgument):
+        hip.matmul(ox.Tensor.empty((4, 4), F32, d), ox.Tensor.empty((4, 4), F32, d), act=ox.ACT_DGELU)
+
+
+def test_host_operand_is_device_mismatch(hip):
+    d = ox.Device.rocm(0)
+    with pytest.raises(ox.DeviceMismatch):
+        hip.matmul(ox.Tensor.empty((4, 4), F32, ox.Device.cpu()), ox.Tensor.empty((4, 4), F32, d))
+
+
+# ---- the north-star configurations ------------------------------------------------------
+
+def check_rows(c_dev, a, b, rows, dtype, k, what):
+    c = to_f32(c_dev).reshape(-1, c_dev.shape[-1])
+    ref = O.matmul(a.ora, b.ora, rows=rows)
+    return assert_close(c[rows], ref, spec_tolerance(dtype, k), what)
+
+
+def check_checksums(c_dev, a, b, k, what):
+    c = to_f32(c_dev)
+    rerr, rscale, cerr, cscale = checksum_residuals(a.logical(), b.logical(), c)
+    # rigorous f32 accumulation bound, summed over the row / column
+    bound = 1.01 * k * 2.0 ** -24
+    assert np.all(rerr <= bound * rscale + 1e-6), f"{what}: row checksum {np.max(rerr / (bound * rscale + 1e-6))}"
+    assert np.all(cerr <= bound * cscale + 1e-6), f"{what}: column checksum {np.max(cerr / (bound * cscale + 1e-6))}"
+
+
+def test_c1_f32_256(hip):
+    rng = np.random.default_rng(1)
+    a = contiguous_operand(F32, rng.uniform(-1, 1, (256, 256)))
+    b = contiguous_operand(F32, rng.uniform(-1, 1, (256, 256)))
+    c = hip.matmul(a.dev, b.dev)
+    assert_close(to_f32(c), O.matmul(a.ora, b.ora), spec_tolerance(F32, 256), "C1")
+
+
+@pytest.mark.parametrize("m,k,n", [(4096, 4096, 4096), (4097, 4093, 4095)], ids=["4096", "odd"])
+def test_c2_f32(hip, m, k, n):
+    rng = np.random.default_rng(2)
+    log(f"C2 f32 {m}x{k}x{n}")
+    a = contiguous_operand(F32, rng.standard_normal((m, k), dtype=np.float32))
+    b = contiguous_operand(F32, rng.standard_normal((k, n), dtype=np.float32))
+    c = hip.matmul(a.dev, b.dev)
+    check_rows(c, a, b, sample_rows(m, 48, 5), F32, k, "C2 rows")
+    check_checksums(c, a, b, k, "C2")
+
+
+def test_c3_bf16_8192_nt(hip):
+    n = 8192
+    rng = np.random.default_rng(3)
+    log("C3 bf16 8192^3, B transposed view")
+    a = Operand(BF16, host_buffer(BF16, rng.normal(0, 0.02, n * n).astype(np.float32)), (n, n), (n, 1))
+    b = Operand(BF16, host_buffer(BF16, rng.normal(0, 0.02, n * n).astype(np.float32)), (n, n), (1, n))
+    c = hip.matmul(a.dev, b.dev, out_dtype=F32)
+    check_rows(c, a, b, sample_rows(n, 24, 6), BF16, n, "C3 rows")
+    check_checksums(c, a, b, n, "C3")
+
+
+def test_c4_batched_broadcast(hip):
+    rng = np.random.default_rng(4)
+    log("C4 batched broadcast")
+    abuf = host_buffer(F32, rng.uniform(-1, 1, 32 * 1024 * 1024).astype(np.float32))
+    a = Operand(F32, abuf, (32, 512, 1024), (1048576, 2048, 1))
+    b = contiguous_operand(F32, rng.uniform(-1, 1, (1, 1024, 768)))
+    c = hip.matmul(a.dev, b.dev)
+    assert c.shape == (32, 512, 768)
+    check_rows(c, a, b, sample_rows(32 * 512, 64, 7, tile=128), F32, 1024, "C4 rows")
+    check_checksums(c, a, b, 1024, "C4")
