@@ -123,8 +123,8 @@ def cpu_baseline(kind: str, host, desc, budget_s: float = 12.0):
 
 
 def kernel_name(kind: str) -> str:
-    return ("gemm_kernel<float,128,128,2,2,Ld::K,Ld::MN>" if kind == "f32"
-            else "gemm_kernel<bf16_t,256,256,2,2,Ld::K,Ld::K>")
+    return ("gemm_kernel<float,128,128,2,2,Ld::K,Ld::MN> (register-staged LDS double buffer)" if kind == "f32"
+            else "gemm_kernel_dl<bf16_t,256,256,2,4,4> (direct-to-LDS ring, 4 stages)")
 
 
 def traffic_for(kind: str):
@@ -164,7 +164,20 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the extra workload")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 256 MiB device copy (10x), the reference for rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE scaling")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        src = torch.empty(64 << 20, dtype=torch.float32, device="cuda:0").normal_()
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "launches": 10}), flush=True)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the GEMM would shard by rows "
               "of A/C, see DESIGN.md); run with --gpus 1", file=sys.stderr)

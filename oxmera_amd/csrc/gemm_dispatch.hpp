@@ -5,13 +5,21 @@
 
 namespace oxm {
 
-constexpr int kSwz = 0;  // LDS XOR pattern (see lds_off)
-
-template <typename T, int BM, int BN, int WM, int WN, Ld LA, Ld LB>
+template <typename T, int BM, int BN, int WM, int WN, Ld LA, Ld LB, bool SCHED = true>
 hipError_t launch_one(const GemmArgs &a, hipStream_t s) {
     int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n * a.batch;
     dim3 grid((unsigned)ntiles), block(WM * WN * 64);
-    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WM, WN, LA, LB, kSwz>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WM, WN, LA, LB, SCHED>), grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
+// Direct-to-LDS kernel (16-bit, both operands K-contiguous).
+template <typename T, int BM, int BN, int WM, int WN, int NS>
+hipError_t launch_dl(GemmArgs a, hipStream_t s) {
+    a.group_m = 4;
+    int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n * a.batch;
+    dim3 grid((unsigned)ntiles), block(WM * WN * 64);
+    hipLaunchKernelGGL((gemm_kernel_dl<T, BM, BN, WM, WN, NS>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 

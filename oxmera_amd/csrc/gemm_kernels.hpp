@@ -31,6 +31,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "gemm_args.hpp"
 
 namespace oxm {
@@ -107,145 +109,188 @@ __device__ __forceinline__ float dgelu_erf(float x) {
 
 // ---- LDS layout ----------------------------------------------------------
 
-// Byte offset of 16-byte chunk `c` (0..7) of K-major row `r` in an operand
-// region.  SWZ selects the XOR pattern (measured with SQ_LDS_BANK_CONFLICT).
-template <int SWZ>
+// Byte offset of 16-byte chunk `c` (0..7) of K-major row `r` (128 B per row)
+// in an operand region.  The LDS serves 256 B per cycle, so a ds_read_b128
+// phase covers 16 lanes: rows are paired into 256-byte lines, the pair's
+// halves are exchanged when bit 3 of the row is set, and chunks are XORed
+// with bits 1..3 of the row.  Then
+//   * fragment reads (16 consecutive rows, one chunk) hit 16 distinct
+//     16-byte bank groups;
+//   * K-loader writes (2 rows x 8 chunks per 16 lanes) and M/N-loader writes
+//     (rows r and r+8 x 8 chunks) do as well.
 __device__ __forceinline__ uint32_t lds_off(int r, int c) {
-    int s = (SWZ == 0) ? (r & 7) : ((r >> 1) & 7);
-    return (uint32_t)(r * 128 + ((c ^ s) << 4));
+    const int half = (r & 1) ^ ((r >> 3) & 1);
+    return (uint32_t)((r >> 1) * 256 + half * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+}
+
+// ---- buffer loads ---------------------------------------------------------
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Byte offsets at or beyond a resource's num_records read as zero; kOob is
+// never inside a resource (num_records <= kMaxRec).
+constexpr uint32_t kMaxRec = 0x7FFFFF00u;
+constexpr uint32_t kOob = 0x7FFFFFF0u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const char *base, int64_t nbytes) {
+    if (nbytes < 0) nbytes = 0;
+    if (nbytes > (int64_t)kMaxRec) nbytes = kMaxRec;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base), (short)0, (int)nbytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 // ---- global -> LDS loaders -----------------------------------------------
 
 // Loads one operand tile (ROWS rows of the M or N dimension, BK = 128 B of K
-// per row) per K step.  `base` already points at (batch, row 0 of the tile,
+// per row) per K step.  `base` points at (batch, first row of the tile,
 // k = 0); `s_mn`/`s_k` are element strides; `rows_left` = rows of the tile
-// that exist (MN - tile origin); K is the full reduction length.
-template <typename T, Ld KIND, int ROWS, int NT, int SWZ>
+// that exist (MN - tile origin); K is the full reduction length.  The host
+// only selects Ld::K / Ld::MN when the strides are non-negative, aligned to
+// 16 bytes and the tile's byte range fits a buffer resource.
+template <typename T, Ld KIND, int ROWS, int NT, int NSET>
 struct Loader;
 
 // K-contiguous rows: thread t owns chunk (t % 8) of rows t/8, t/8 + NT/8, ...
-template <typename T, int ROWS, int NT, int SWZ>
-struct Loader<T, Ld::K, ROWS, NT, SWZ> {
+template <typename T, int ROWS, int NT, int NSET>
+struct Loader<T, Ld::K, ROWS, NT, NSET> {
     static constexpr int kBytes = Elem<T>::kBytes;
     static constexpr int kVec = 16 / kBytes;
     static constexpr int kBK = 128 / kBytes;
     static constexpr int kPer = ROWS * 8 / NT;
     static_assert(ROWS * 8 % NT == 0, "tile rows must cover the workgroup");
+    static constexpr int kVmem = kPer, kDsWrite = kPer;  // instructions per K step
     const char *base;
-    int64_t row_off[kPer];  // byte offsets of this thread's rows
-    bool row_ok[kPer];
+    int64_t nbytes;
+    uint32_t off[kPer];  // byte offsets of this thread's chunks (kOob: row absent)
     int chunk;
     int64_t K;
-    uint4 regs[kPer];
+    uint4 regs[NSET][kPer];  // staging sets (NSET = prefetch distance)
 
     __device__ __forceinline__ Loader(const char *b, int64_t s_mn, int64_t /*s_k*/, int64_t rows_left, int64_t k,
                                       int tid)
         : base(b), K(k) {
         chunk = tid & 7;
+        const int64_t rows_here = rows_left < ROWS ? rows_left : ROWS;
+        nbytes = ((rows_here - 1) * s_mn + k) * kBytes;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             int r = (tid >> 3) + i * (NT / 8);
-            row_off[i] = (int64_t)r * s_mn * kBytes + chunk * 16;
-            row_ok[i] = r < rows_left;
+            off[i] = r < rows_left ? (uint32_t)(r * s_mn * kBytes + chunk * 16) : kOob;
         }
     }
+    template <int S>
     __device__ __forceinline__ void prefetch(int kt) {
-        int64_t k0 = (int64_t)kt * kBK;
-        bool k_ok = k0 + chunk * kVec < K;
+        const int64_t k0 = (int64_t)kt * kBK;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + k0 * kBytes, nbytes - k0 * kBytes);
+        const bool k_ok = (k0 + kBK <= K) || (k0 + chunk * kVec < K);
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            if (row_ok[i] && k_ok)
-                regs[i] = *(const uint4 *)(base + row_off[i] + k0 * kBytes);
-            else
-                regs[i] = make_uint4(0, 0, 0, 0);
-        }
+        for (int i = 0; i < kPer; ++i) regs[S][i] = buf_load16(rs, k_ok ? off[i] : kOob);
     }
+    template <int S>
     __device__ __forceinline__ void store(uint8_t *lds, int tid, int /*kt*/) {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             int r = (tid >> 3) + i * (NT / 8);
-            *(uint4 *)(lds + lds_off<SWZ>(r, chunk)) = regs[i];
+            *(uint4 *)(lds + lds_off(r, chunk)) = regs[S][i];
         }
     }
 };
 
-// M/N-contiguous columns: thread t owns a kVec(mn) x kVec(k) block: k-block
-// t % 8, mn-block t / 8 (+ NT/8 per repeat).  kVec 16-byte loads along MN,
-// transposed in registers into kVec K-major 16-byte chunks.
-template <typename T, int ROWS, int NT, int SWZ>
-struct Loader<T, Ld::MN, ROWS, NT, SWZ> {
+// M/N-contiguous columns: thread t owns a kVec(mn) x kVec(k) block, k-block
+// t % 8; kVec 16-byte loads along MN are transposed in registers into kVec
+// K-major 16-byte chunks.  Blocks are assigned so that the two 8-lane halves
+// of every 16-lane LDS phase write rows 8 apart (opposite bank halves).
+template <typename T, int ROWS, int NT, int NSET>
+struct Loader<T, Ld::MN, ROWS, NT, NSET> {
     static constexpr int kBytes = Elem<T>::kBytes;
     static constexpr int kVec = 16 / kBytes;
     static constexpr int kBK = 128 / kBytes;
     static constexpr int kBlocks = (ROWS / kVec) * 8;
     static constexpr int kPer = kBlocks >= NT ? kBlocks / NT : 1;
     static_assert(kBlocks % NT == 0 || NT % kBlocks == 0, "block count must tile the workgroup");
+    static constexpr int kVmem = kPer * kVec, kDsWrite = kPer * kVec;
     const char *base;
-    int64_t s_k_bytes;
-    int64_t blk_off[kPer];
-    bool blk_ok[kPer];
+    int64_t nbytes, sk_bytes;
+    uint32_t off[kPer];
+    int mb[kPer];
+    bool ok[kPer];
     bool active;
     int kb;
     int64_t K;
-    uint4 regs[kPer][kVec];
+    uint4 regs[NSET][kPer][kVec];
+
+    __device__ __forceinline__ static int block_of(int q) {
+        if constexpr (kVec == 8) {
+            return q;  // rows 8q..8q+7: neighbours q, q+1 are 8 rows apart
+        } else {
+            // 4-row blocks: pair q = 2j + s with blocks j' and j' + 2 (8 rows apart)
+            const int j = (q & 7) >> 1, s = q & 1;
+            return (q & ~7) + (j & 1) + 4 * (j >> 1) + 2 * s;
+        }
+    }
 
     __device__ __forceinline__ Loader(const char *b, int64_t /*s_mn*/, int64_t s_k, int64_t rows_left, int64_t k,
                                       int tid)
         : base(b), K(k) {
-        s_k_bytes = s_k * kBytes;
+        sk_bytes = s_k * kBytes;
         kb = tid & 7;
         active = tid < kBlocks * kPer;
+        const int64_t rows_here = rows_left < ROWS ? rows_left : ROWS;
+        nbytes = (k - 1) * sk_bytes + rows_here * kBytes;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            int mb = (tid >> 3) + i * (NT / 8);
-            blk_off[i] = (int64_t)mb * 16 + (int64_t)kb * kVec * s_k_bytes;
-            blk_ok[i] = active && (int64_t)mb * kVec < rows_left;
+            mb[i] = block_of((tid >> 3) + i * (NT / 8));
+            ok[i] = active && (int64_t)mb[i] * kVec < rows_left;
+            off[i] = (uint32_t)(mb[i] * 16 + kb * kVec * sk_bytes);
         }
     }
+    template <int S>
     __device__ __forceinline__ void prefetch(int kt) {
-        int64_t k0 = (int64_t)kt * kBK;
+        const int64_t k0 = (int64_t)kt * kBK;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + k0 * sk_bytes, nbytes - k0 * sk_bytes);
+        const bool full = k0 + kBK <= K;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const char *p = base + blk_off[i] + k0 * s_k_bytes;
 #pragma unroll
             for (int j = 0; j < kVec; ++j) {
-                if (blk_ok[i] && k0 + kb * kVec + j < K)
-                    regs[i][j] = *(const uint4 *)(p + j * s_k_bytes);
-                else
-                    regs[i][j] = make_uint4(0, 0, 0, 0);
+                const bool v = ok[i] && (full || k0 + kb * kVec + j < K);
+                regs[S][i][j] = buf_load16(rs, v ? off[i] + (uint32_t)(j * sk_bytes) : kOob);
             }
         }
     }
-    __device__ __forceinline__ void store(uint8_t *lds, int tid, int /*kt*/) {
+    template <int S>
+    __device__ __forceinline__ void store(uint8_t *lds, int /*tid*/, int /*kt*/) {
         if (!active) return;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            int mb = (tid >> 3) + i * (NT / 8);
             if constexpr (kBytes == 4) {
-                // 4x4 f32 transpose: pure register renaming.
-                const uint32_t *in = (const uint32_t *)regs[i];
+                // 4x4 f32 transpose: register renaming only.
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    uint4 v = make_uint4(in[0 * 4 + r], in[1 * 4 + r], in[2 * 4 + r], in[3 * 4 + r]);
-                    *(uint4 *)(lds + lds_off<SWZ>(mb * 4 + r, kb)) = v;
+                    uint4 v;
+                    v.x = (&regs[S][i][0].x)[r];
+                    v.y = (&regs[S][i][1].x)[r];
+                    v.z = (&regs[S][i][2].x)[r];
+                    v.w = (&regs[S][i][3].x)[r];
+                    *(uint4 *)(lds + lds_off(mb[i] * 4 + r, kb)) = v;
                 }
             } else {
-                // 8x8 16-bit transpose: out row r, dword d = (in[2d][r], in[2d+1][r]).
-                const uint32_t *in = (const uint32_t *)regs[i];  // in[j*4 + w]: k=j, mn=2w,2w+1
+                // 8x8 16-bit transpose: output row r, dword d = (in[2d][r], in[2d+1][r]).
 #pragma unroll
                 for (int r = 0; r < 8; ++r) {
                     uint32_t o[4];
 #pragma unroll
                     for (int d = 0; d < 4; ++d) {
-                        uint32_t lo = in[(2 * d) * 4 + (r >> 1)];
-                        uint32_t hi = in[(2 * d + 1) * 4 + (r >> 1)];
-                        if (r & 1)
-                            o[d] = (lo >> 16) | (hi & 0xffff0000u);
-                        else
-                            o[d] = (lo & 0xffffu) | (hi << 16);
+                        const uint32_t lo = (&regs[S][i][2 * d].x)[r >> 1];
+                        const uint32_t hi = (&regs[S][i][2 * d + 1].x)[r >> 1];
+                        o[d] = (r & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
                     }
-                    *(uint4 *)(lds + lds_off<SWZ>(mb * 8 + r, kb)) = make_uint4(o[0], o[1], o[2], o[3]);
+                    *(uint4 *)(lds + lds_off(mb[i] * 8 + r, kb)) = make_uint4(o[0], o[1], o[2], o[3]);
                 }
             }
         }
@@ -254,13 +299,14 @@ struct Loader<T, Ld::MN, ROWS, NT, SWZ> {
 
 // Generic strided operand: element loads with full bounds checks, issued in
 // the store phase (no register staging).  Threads walk the operand's
-// unit-ish dimension so neighbouring lanes touch neighbouring addresses.
-template <typename T, int ROWS, int NT, int SWZ>
-struct Loader<T, Ld::G, ROWS, NT, SWZ> {
+// smaller-stride dimension so neighbouring lanes touch neighbouring addresses.
+template <typename T, int ROWS, int NT, int NSET>
+struct Loader<T, Ld::G, ROWS, NT, NSET> {
     static constexpr int kBytes = Elem<T>::kBytes;
     static constexpr int kVec = 16 / kBytes;
     static constexpr int kBK = 128 / kBytes;
     static constexpr int kPer = ROWS * kBK / NT;
+    static constexpr int kVmem = -1, kDsWrite = -1;  // data-dependent: no fixed schedule
     const char *base;
     int64_t s_mn, s_k, rows_left, K;
     bool along_k;
@@ -270,12 +316,14 @@ struct Loader<T, Ld::G, ROWS, NT, SWZ> {
         int64_t am = smn < 0 ? -smn : smn, ak = sk < 0 ? -sk : sk;
         along_k = ak <= am;
     }
+    template <int S>
     __device__ __forceinline__ void prefetch(int) {}
+    template <int S>
     __device__ __forceinline__ void store(uint8_t *lds, int tid, int kt) {
-        int64_t k0 = (int64_t)kt * kBK;
+        const int64_t k0 = (int64_t)kt * kBK;
 #pragma unroll 4
         for (int i = 0; i < kPer; ++i) {
-            int e = tid + i * NT;
+            const int e = tid + i * NT;
             int r, kk;
             if (along_k) {
                 r = e / kBK;
@@ -284,15 +332,15 @@ struct Loader<T, Ld::G, ROWS, NT, SWZ> {
                 r = e % ROWS;
                 kk = e / ROWS;
             }
-            bool ok = r < rows_left && k0 + kk < K;
+            const bool ok = r < rows_left && k0 + kk < K;
             const char *p = base + ((int64_t)r * s_mn + (k0 + kk) * s_k) * kBytes;
-            uint32_t off = lds_off<SWZ>(r, kk / kVec) + (kk % kVec) * kBytes;
+            const uint32_t o = lds_off(r, kk / kVec) + (kk % kVec) * kBytes;
             if constexpr (kBytes == 4) {
                 float v = ok ? *(const float *)p : 0.0f;
-                *(float *)(lds + off) = v;
+                *(float *)(lds + o) = v;
             } else {
                 uint16_t v = ok ? *(const uint16_t *)p : (uint16_t)0;
-                *(uint16_t *)(lds + off) = v;
+                *(uint16_t *)(lds + o) = v;
             }
         }
     }
@@ -408,7 +456,7 @@ __device__ __forceinline__ void write_slab(const GemmArgs &p, const float *ws, i
                                            int64_t col0, int lane) {
     constexpr int kLanesPerRow = WN / 4;
     constexpr int kRowsPerIter = 64 / kLanesPerRow;
-    constexpr int kSld = WN + 4;
+    constexpr int kSld = WN + 8;
     const int c4 = (lane % kLanesPerRow) * 4;
     const int64_t col = col0 + c4;
     const int nvalid = (int)(p.N - col < 4 ? (p.N - col < 0 ? 0 : p.N - col) : 4);
@@ -425,7 +473,15 @@ __device__ __forceinline__ void write_slab(const GemmArgs &p, const float *ws, i
 
 // ---- the kernel -------------------------------------------------------------
 
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, Ld LA, Ld LB, int SWZ>
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, Ld LA, Ld LB, bool SCHED = true, int PF = 1>
 __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p) {
     constexpr int NT = WAVES_M * WAVES_N * 64;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
@@ -433,8 +489,9 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
     constexpr int kBytes = Elem<T>::kBytes;
     constexpr int kBK = 128 / kBytes;
     constexpr int kRegionA = BM * 128, kRegionB = BN * 128;
+    constexpr int kStage = kRegionA + kRegionB;  // bytes per LDS buffer
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * (kRegionA + kRegionB)];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStage];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -457,18 +514,21 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
     const int64_t tile_n = tin / gm;
     const int64_t m0 = tile_m * BM, n0 = tile_n * BN;
 
-    int64_t offa = 0, offb = 0, rem = bidx;
-    for (int d = p.nbd - 1; d >= 0; --d) {
-        int64_t i = rem % p.bext[d];
-        rem /= p.bext[d];
-        offa += i * p.bsa[d];
-        offb += i * p.bsb[d];
+    int64_t offa = 0, offb = 0;
+    if (p.nbd > 0) {
+        int64_t rem = bidx;
+        for (int d = p.nbd - 1; d >= 0; --d) {
+            int64_t i = rem % p.bext[d];
+            rem /= p.bext[d];
+            offa += i * p.bsa[d];
+            offb += i * p.bsb[d];
+        }
     }
     const char *abase = (const char *)p.a + (offa + m0 * p.sam) * kBytes;
     const char *bbase = (const char *)p.b + (offb + n0 * p.sbn) * kBytes;
 
-    Loader<T, LA, BM, NT, SWZ> la(abase, p.sam, p.sak, p.M - m0, p.K, tid);
-    Loader<T, LB, BN, NT, SWZ> lb(bbase, p.sbn, p.sbk, p.N - n0, p.K, tid);
+    Loader<T, LA, BM, NT, PF> la(abase, p.sam, p.sak, p.M - m0, p.K, tid);
+    Loader<T, LB, BN, NT, PF> lb(bbase, p.sbn, p.sbk, p.N - n0, p.K, tid);
 
     f32x16_t acc[TM][TN];
 #pragma unroll
@@ -476,58 +536,92 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x16_t{};
 
-    const int nk = (int)((p.K + kBK - 1) / kBK);
-    constexpr int kStage = kRegionA + kRegionB;  // bytes per LDS buffer
-
-    if (nk > 0) {
-        la.prefetch(0);
-        lb.prefetch(0);
-        la.store(lds, tid, 0);
-        lb.store(lds + kRegionA, tid, 0);
-        __syncthreads();
-    }
+    // Fragment addressing: lane l reads chunk 2g + l/32 of row (base + l%32 +
+    // 32 i); rows 32 apart share the swizzle, so tile i adds i * 4096 bytes.
+    const int half = lane >> 5;
     const int arow = wm * WM + (lane & 31);
     const int brow = wn * WN + (lane & 31);
-    const int half = lane >> 5;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) {
-            la.prefetch(kt + 1);
-            lb.prefetch(kt + 1);
+    uint32_t aoff[4], boff[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        aoff[g] = lds_off(arow, 2 * g + half);
+        boff[g] = kRegionA + lds_off(brow, 2 * g + half);
+    }
+    uint4 fa[2][TM], fb[2][TN];
+    auto read_frags = [&](const uint8_t *stage, int g, uint4(&A)[TM], uint4(&B)[TN]) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) A[i] = *(const uint4 *)(stage + aoff[g] + i * 4096);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) B[j] = *(const uint4 *)(stage + boff[g] + j * 4096);
+    };
+
+    // Pipeline: LDS double buffer (stage kt&1 is computed while stage
+    // (kt+1)&1 is filled) and PF register sets for the global loads: step
+    // kt+PF is loaded into set (kt+PF)%PF while set (kt+1)%PF is stored.
+    // Order of one K step, pinned with scheduling fences (without them the
+    // compiler sinks the global loads next to their LDS stores and exposes
+    // the full memory latency every step):
+    //   global loads of step kt+PF
+    //   for g = 0..3: LDS reads of group g+1, MFMAs of group g
+    //   LDS stores of step kt+1, barrier, LDS reads of group 0 of kt+1.
+    // Loads past the end of K are out of range and read zeros.
+    static_assert(PF == 1 || PF == 2, "prefetch distance 1 or 2");
+    const int nk = (int)((p.K + kBK - 1) / kBK);
+    if (nk > 0) {
+        la.template prefetch<0>(0);
+        lb.template prefetch<0>(0);
+        la.template store<0>(lds, tid, 0);
+        lb.template store<0>(lds + kRegionA, tid, 0);
+        if constexpr (PF == 2) {
+            la.template prefetch<1>(1);
+            lb.template prefetch<1>(1);
         }
-        const uint8_t *sa = lds + cur * kStage;
-        const uint8_t *sb = sa + kRegionA;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            uint4 af[TM], bfr[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) af[i] = *(const uint4 *)(sa + lds_off<SWZ>(arow + i * 32, 2 * g + half));
-#pragma unroll
-            for (int j = 0; j < TN; ++j) bfr[j] = *(const uint4 *)(sb + lds_off<SWZ>(brow + j * 32, 2 * g + half));
+        __syncthreads();
+        read_frags(lds, 0, fa[0], fb[0]);
+    }
+    auto k_step = [&](auto sc, int kt) {
+        constexpr int S = decltype(sc)::value;  // kt % 2 for PF == 2
+        const int cur = PF == 2 ? S : (kt & 1);
+        const uint8_t *stage = lds + cur * kStage;
+        uint8_t *nxt = lds + (cur ^ 1) * kStage;
+        constexpr int kLoadSet = PF == 2 ? S : 0, kStoreSet = PF == 2 ? (S ^ 1) : 0;
+        la.template prefetch<kLoadSet>(kt + PF);
+        lb.template prefetch<kLoadSet>(kt + PF);
+        if constexpr (SCHED) __builtin_amdgcn_sched_barrier(0);
+        static_for<0, 4>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            if constexpr (g < 3) read_frags(stage, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j) Mma<T>::run(acc[i][j], af[i], bfr[j]);
-        }
-        if (kt + 1 < nk) {
-            uint8_t *nxt = lds + (cur ^ 1) * kStage;
-            la.store(nxt, tid, kt + 1);
-            lb.store(nxt + kRegionA, tid, kt + 1);
-        }
+                for (int j = 0; j < TN; ++j) Mma<T>::run(acc[i][j], fa[g & 1][i], fb[g & 1][j]);
+            if constexpr (SCHED) __builtin_amdgcn_sched_barrier(0);
+        });
+        la.template store<kStoreSet>(nxt, tid, kt + 1);
+        lb.template store<kStoreSet>(nxt + kRegionA, tid, kt + 1);
         __syncthreads();
+        read_frags(nxt, 0, fa[0], fb[0]);
+    };
+    if constexpr (PF == 2) {
+        for (int kt = 0; kt < nk; kt += 2) {
+            k_step(std::integral_constant<int, 0>{}, kt);
+            if (kt + 1 < nk) k_step(std::integral_constant<int, 1>{}, kt + 1);
+        }
+    } else {
+        for (int kt = 0; kt < nk; ++kt) k_step(std::integral_constant<int, 0>{}, kt);
     }
 
     // Epilogue: each wave stages one 32-row slab of its accumulators in LDS
     // (the operand buffers are free after the last barrier), then stores it
     // row-contiguously.  32x32 MFMA accumulator layout: lane l, element e is
     // C[8*(e/4) + 4*(l/32) + e%4][l%32].
-    constexpr int kSld = WN + 4;
-    static_assert(NT / 64 * 32 * kSld * 4 <= 2 * (kRegionA + kRegionB), "epilogue staging must fit in LDS");
+    constexpr int kSld = WN + 8;  // rows 4 apart land on opposite bank halves
+    static_assert(NT / 64 * 32 * kSld * 4 <= 2 * kStage, "epilogue staging must fit in LDS");
     float *ws = (float *)lds + wave * 32 * kSld;
     const int64_t cbase = bidx * p.M * p.N;
     const int64_t col0 = n0 + wn * WN;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    static_for<0, TM>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
@@ -542,7 +636,210 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
         else
             write_slab<kDtF16, WN>(p, ws, cbase, row0, col0, lane);
         __syncthreads();
+    });
+}
+
+// ===========================================================================
+// Direct-to-LDS pipeline for 16-bit operands that are both K-contiguous.
+//
+// The register-staged kernel above keeps one K step (64 KB for a 256x256
+// tile) in flight per CU, and at 8192^3 that leaves the MFMAs waiting on
+// global-load latency.  Here global loads go straight into LDS
+// (buffer_load_dwordx4 ... lds: no VGPR staging, no ds_write) and the LDS is
+// a ring of NS stages of 32 k each, so NS-1 stages (96-128 KB) are in flight
+// while one is consumed.  One barrier per stage.
+// ===========================================================================
+
+// LDS layout of a stage: 64-byte rows (32 k of a 16-bit type, four 16-byte
+// chunks), four rows per 256-byte line.  Position of chunk c of row r in its
+// line: (r % 4) * 4 + (c ^ ((r / 4) % 4)).  A fragment read (16 consecutive
+// rows, one chunk) covers all 16 positions of the 256-byte bank width.
+__device__ __forceinline__ uint32_t lds_off64(int r, int c) {
+    return (uint32_t)((r >> 2) * 256 + (((r & 3) << 2) | (c ^ ((r >> 2) & 3))) * 16);
+}
+
+// s_waitcnt immediate that waits for vmcnt <= n and nothing else (gfx9
+// encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+constexpr int waitcnt_vm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
+
+// One operand tile of ROWS rows: each wave instruction fills one 1 KB block
+// (16 rows x 64 B) of the stage; lane L of block b reads row
+// 16 b + 4 (L / 16) + (L % 16) / 4, chunk (L % 4) ^ (L / 16).
+template <int ROWS, int NT>
+struct DirectLoader {
+    static constexpr int kWaves = NT / 64;
+    static constexpr int kBlocks = ROWS / 16;
+    static constexpr int kPer = kBlocks / kWaves;  // load instructions per wave per stage
+    static_assert(kBlocks % kWaves == 0, "blocks must divide among the waves");
+    const char *base;
+    int64_t nbytes, K;
+    uint32_t voff[kPer];
+    int chunk;
+
+    __device__ __forceinline__ DirectLoader(const char *b, int64_t s_mn, int64_t rows_left, int64_t k, int wave,
+                                            int lane)
+        : base(b), K(k) {
+        const int line = lane >> 4, pos = lane & 15;
+        chunk = (pos & 3) ^ line;
+        const int64_t rows_here = rows_left < ROWS ? rows_left : ROWS;
+        nbytes = ((rows_here - 1) * s_mn + k) * 2;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int blk = wave + i * kWaves;
+            const int r = blk * 16 + line * 4 + (pos >> 2);
+            voff[i] = r < rows_left ? (uint32_t)(r * s_mn * 2 + chunk * 16) : kOob;
+        }
     }
+    // Issue the loads of K step kt (32 k) into the stage at `dst`.  Written
+    // as inline asm so the compiler does not treat the DMA as an LDS store
+    // it must wait for before every LDS read; the kernel orders it
+    // explicitly (s_waitcnt vmcnt + s_barrier).
+    __device__ __forceinline__ void issue(uint8_t *dst, int kt, int wave) {
+        const int64_t k0 = (int64_t)kt * 32;
+        int64_t nb = nbytes - k0 * 2;
+        nb = nb < 0 ? 0 : (nb > (int64_t)kMaxRec ? (int64_t)kMaxRec : nb);
+        const uint64_t addr = (uint64_t)(base + k0 * 2);
+        i32x4_t rsrc;
+        rsrc.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
+        rsrc.y = __builtin_amdgcn_readfirstlane((int)(uint32_t)(addr >> 32) & 0xffff);
+        rsrc.z = __builtin_amdgcn_readfirstlane((int)nb);
+        rsrc.w = 0x00020000;
+        const bool k_ok = k0 + chunk * 8 < K;
+        const uint32_t lds_base = (uint32_t)(uintptr_t)dst;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int blk = wave + i * kWaves;
+            const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_base + blk * 1024);
+            const uint32_t vo = k_ok ? voff[i] : kOob;
+            asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(vo), "s"(rsrc), "{m0}"(m0) : "memory");
+        }
+    }
+};
+
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int NS>
+__global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dl(GemmArgs p) {
+    constexpr int NT = WAVES_M * WAVES_N * 64;
+    constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int kStageA = BM * 64, kStageB = BN * 64;
+    constexpr int kStage = kStageA + kStageB;
+    static_assert(Elem<T>::kBytes == 2, "direct-to-LDS path is for 16-bit operands");
+    static_assert(NS >= 3, "at least three stages");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+
+    const int64_t per_batch = (int64_t)p.tiles_m * p.tiles_n;
+    const int64_t ntiles = per_batch * p.batch;
+    int64_t wg = blockIdx.x;
+    if (p.xcd_remap && (ntiles & 7) == 0) wg = (wg & 7) * (ntiles >> 3) + (wg >> 3);
+    const int64_t bidx = wg / per_batch;
+    const int64_t t = wg - bidx * per_batch;
+    const int64_t gsz = (int64_t)p.group_m * p.tiles_n;
+    const int64_t grp = t / gsz;
+    const int64_t first_m = grp * p.group_m;
+    const int64_t gm = (p.tiles_m - first_m) < p.group_m ? (p.tiles_m - first_m) : p.group_m;
+    const int64_t tin = t - grp * gsz;
+    const int64_t tile_m = first_m + tin % gm;
+    const int64_t tile_n = tin / gm;
+    const int64_t m0 = tile_m * BM, n0 = tile_n * BN;
+    int64_t offa = 0, offb = 0;
+    if (p.nbd > 0) {
+        int64_t rem = bidx;
+        for (int d = p.nbd - 1; d >= 0; --d) {
+            int64_t i = rem % p.bext[d];
+            rem /= p.bext[d];
+            offa += i * p.bsa[d];
+            offb += i * p.bsb[d];
+        }
+    }
+    DirectLoader<BM, NT> la((const char *)p.a + (offa + m0 * p.sam) * 2, p.sam, p.M - m0, p.K, wave, lane);
+    DirectLoader<BN, NT> lb((const char *)p.b + (offb + n0 * p.sbn) * 2, p.sbn, p.N - n0, p.K, wave, lane);
+    constexpr int kLoadsPerStage = DirectLoader<BM, NT>::kPer + DirectLoader<BN, NT>::kPer;
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x16_t{};
+
+    // Fragment g (16 k) of a stage: lane l reads chunk 2g + l/32 of row
+    // base + l%32; rows 32 apart are 2048 bytes apart in this layout.
+    const int half = lane >> 5;
+    const int arow = wm * WM + (lane & 31);
+    const int brow = wn * WN + (lane & 31);
+    uint32_t aoff[2], boff[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        aoff[g] = lds_off64(arow, 2 * g + half);
+        boff[g] = kStageA + lds_off64(brow, 2 * g + half);
+    }
+    uint4 fa[2][TM], fb[2][TN];
+    auto read_frags = [&](const uint8_t *stage, int g, uint4(&A)[TM], uint4(&B)[TN]) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) A[i] = *(const uint4 *)(stage + aoff[g] + i * 2048);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) B[j] = *(const uint4 *)(stage + boff[g] + j * 2048);
+    };
+
+    const int nk = (int)((p.K + 31) / 32);
+    // Prologue: stages 0 .. NS-2 in flight.
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) {
+        la.issue(lds + s * kStage, s, wave);
+        lb.issue(lds + s * kStage + kStageA, s, wave);
+    }
+    int cur = 0;  // stage of step kt
+    for (int kt = 0; kt < nk; ++kt) {
+        // Step kt's loads are the oldest NS-1 stages ago: wait for them, then
+        // the barrier makes every wave's part visible and frees stage kt-1.
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * kLoadsPerStage));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        int nxt = cur == 0 ? NS - 1 : cur - 1;  // (kt + NS - 1) % NS
+        la.issue(lds + nxt * kStage, kt + NS - 1, wave);
+        lb.issue(lds + nxt * kStage + kStageA, kt + NS - 1, wave);
+        const uint8_t *stage = lds + cur * kStage;
+        read_frags(stage, 0, fa[0], fb[0]);
+        read_frags(stage, 1, fa[1], fb[1]);
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) Mma<T>::run(acc[i][j], fa[g][i], fb[g][j]);
+        cur = cur + 1 == NS ? 0 : cur + 1;
+    }
+    // Loads past the end of K were issued (out of range: they write zeros to
+    // LDS); drain them before the LDS is reused for the epilogue.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();
+
+    constexpr int kSld = WN + 8;
+    static_assert(NT / 64 * 32 * kSld * 4 <= NS * kStage, "epilogue staging must fit in LDS");
+    float *ws = (float *)lds + wave * 32 * kSld;
+    const int64_t cbase = bidx * p.M * p.N;
+    const int64_t col0 = n0 + wn * WN;
+    static_for<0, TM>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                ws[(8 * (e >> 2) + 4 * half + (e & 3)) * kSld + j * 32 + (lane & 31)] = acc[i][j][e];
+        __syncthreads();
+        const int64_t row0 = m0 + wm * WM + i * 32;
+        if (p.out_dtype == kDtF32)
+            write_slab<kDtF32, WN>(p, ws, cbase, row0, col0, lane);
+        else if (p.out_dtype == kDtBF16)
+            write_slab<kDtBF16, WN>(p, ws, cbase, row0, col0, lane);
+        else
+            write_slab<kDtF16, WN>(p, ws, cbase, row0, col0, lane);
+        __syncthreads();
+    });
 }
 
 }  // namespace oxm

@@ -14,6 +14,10 @@ enum TileCfg : int {
     kCfgF32_128 = 0,   // f32: 128x128 tile, 2x2 waves of 64x64, BK 32
     kCfgH_256 = 1,     // bf16/f16: 256x256 tile, 2x2 waves of 128x128, BK 64
     kCfgH_128 = 2,     // bf16/f16: 128x128 tile, 2x2 waves of 64x64, BK 64
+                       // (K-contiguous A and B use the direct-to-LDS ring:
+                       //  256x256 = 2x4 waves, 4 stages of 32 k; 128x128 = 2x2 waves)
+    // tuning variant (16-bit, K-contiguous A and B; selected by OXM_GEMM_CFG)
+    kCfgH_256_NS = 4,  // 256x256 register-staged kernel instead of the direct-to-LDS one
 };
 
 struct TileShape {

@@ -177,17 +177,24 @@ oxm_status finish(hipStream_t s, const char *op) {
     return ok();
 }
 
-// Operand loader choice from the view's strides (see gemm_kernels.hpp).
+// Operand loader choice from the view's strides (see gemm_kernels.hpp).  The
+// vector loaders read through a 32-bit buffer resource per tile, so they
+// also need non-negative strides and a tile byte range below 2^31.
 int classify(const char *ptr, int64_t s_mn, int64_t s_k, int64_t mn, int64_t k, const int64_t *bstr, int nbd,
-             int es) {
+             int es, int tile_rows) {
     const int64_t vec = 16 / es;
+    const int64_t kMaxRec = 0x7FFFFF00LL;
     bool aligned = ((uintptr_t)ptr % 16) == 0;
     bool batch_ok = true;
     for (int d = 0; d < nbd; ++d) batch_ok = batch_ok && (bstr[d] % vec == 0);
     if (mn == 1) s_mn = 0;
     if (k == 1) s_k = 0;
-    if (aligned && batch_ok && s_k == 1 && k % vec == 0 && s_mn % vec == 0) return oxm::kLdK;
-    if (aligned && batch_ok && s_mn == 1 && mn % vec == 0 && s_k % vec == 0) return oxm::kLdMN;
+    if (aligned && batch_ok && s_k == 1 && k % vec == 0 && s_mn % vec == 0 && s_mn >= 0 &&
+        ((int64_t)tile_rows * s_mn + k) * es <= kMaxRec)
+        return oxm::kLdK;
+    if (aligned && batch_ok && s_mn == 1 && mn % vec == 0 && s_k % vec == 0 && s_k >= 0 &&
+        (k * s_k + tile_rows) * es <= kMaxRec)
+        return oxm::kLdMN;
     return oxm::kLdG;
 }
 
@@ -347,8 +354,6 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     g.out_dtype = c->dtype;
     g.bias_dtype = ep->bias_dtype;
 
-    int ld_a = classify((const char *)g.a, g.sam, g.sak, M, K, g.bsa, nbd, es);
-    int ld_b = classify((const char *)g.b, g.sbn, g.sbk, N, K, g.bsb, nbd, es);
     int cfg;
     if (a->dtype == OXM_F32) {
         cfg = oxm::kCfgF32_128;
@@ -356,9 +361,11 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
         int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
         cfg = big_tiles >= 256 ? oxm::kCfgH_256 : oxm::kCfgH_128;
         cfg = env_int("OXM_GEMM_CFG", cfg);
-        if (cfg != oxm::kCfgH_256 && cfg != oxm::kCfgH_128) cfg = oxm::kCfgH_128;
+        if (cfg != oxm::kCfgH_256 && cfg != oxm::kCfgH_128 && cfg != oxm::kCfgH_256_NS) cfg = oxm::kCfgH_128;
     }
     oxm::TileShape ts = oxm::tile_shape(cfg);
+    int ld_a = classify((const char *)g.a, g.sam, g.sak, M, K, g.bsa, nbd, es, ts.bm);
+    int ld_b = classify((const char *)g.b, g.sbn, g.sbk, N, K, g.bsb, nbd, es, ts.bn);
     int64_t ntiles = ((M + ts.bm - 1) / ts.bm) * ((N + ts.bn - 1) / ts.bn) * batch;
     if (ntiles > 0x7fffffffLL) return fail(OXM_E_NOT_IMPLEMENTED, "matmul is not implemented for %lld tiles", (long long)ntiles);
     hipStream_t s = (hipStream_t)stream;
