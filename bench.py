@@ -94,6 +94,41 @@ def time_gpu(kind: str, steps: int, warmup: int):
     return dict(total_ms=total_ms, per_ms=per_ms, flops=flops, desc=desc, host=host, out=out, a=a, b=b)
 
 
+def time_mlp(steps: int, warmup: int):
+    """one MLP training step (forward, MSE, backward) through the
+    autograd tape: X [8192, 4096] bf16, Linear 4096->16384 + bias + GELU,
+    Linear 16384->4096 + bias.  Six GEMMs of 2*8192*4096*16384 flops each."""
+    import torch
+    import oxmera_amd as ox
+    from oxmera_amd.autograd import Var
+    from oxmera_amd.nn import MLP2, Linear
+    ox.init()
+    dev = ox.Device.rocm(0)
+    rng = np.random.default_rng(777)
+    n, d, h = 8192, 4096, 16384
+    bf = lambda a: ox.Tensor.from_numpy(a.astype(np.float32), dev, ox.DType.BF16)
+    fc1 = Linear(bf(rng.normal(0, 0.02, (d, h))), bf(rng.normal(0, 0.02, h)), act=ox.ACT_GELU)
+    fc2 = Linear(bf(rng.normal(0, 0.02, (h, d))), bf(rng.normal(0, 0.02, d)))
+    model = MLP2(fc1, fc2)
+    x = Var(bf(rng.normal(0, 1, (n, d))), requires_grad=True)
+    t = bf(rng.normal(0, 1, (n, d)))
+    for _ in range(warmup):
+        model.train_step(x, t)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = model.train_step(x, t)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    flops = 6 * 2.0 * n * d * h
+    return {"config": {"workload": "MLP fwd+bwd, X [8192,4096] bf16, 4096->16384 (+bias, GELU) ->4096 (+bias), "
+                                   "MSE (BASELINE configs[4]); synchronous host calls (null stream)",
+                       "gemm_flops_per_step": flops},
+            "ms_per_step": round(dt * 1e3, 3), "value": round(flops / dt / 1e12, 1), "unit": "TFLOP/s (6 GEMMs)",
+            "pct_of_peak": round(100 * flops / dt / 1e12 / PEAK["bf16"], 2),
+            "loss": float(loss.t.to_numpy()[0])}
+
+
 def cpu_baseline(kind: str, host, desc, budget_s: float = 12.0):
     """The naive oracle on a bounded sample of output rows, all host threads."""
     from oracle import oracle as O
@@ -219,6 +254,8 @@ def main():
                                  "ms_per_step": round(r2["total_ms"] / r2["steps"], 4),
                                  "median_launch_ms": round(r2["per_ms"][len(r2["per_ms"]) // 2], 4),
                                  "roofline": roofline(other, r2)}}
+        del r2
+        line["extra"]["mlp"] = time_mlp(max(3, args.steps // 10), 1)
     print(json.dumps(line), flush=True)
 
 
