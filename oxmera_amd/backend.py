@@ -24,10 +24,24 @@ from .tensor import Tensor
 
 
 class HipBackend:
-    """MI355X (gfx950) backend for one HIP device."""
+    """MI355X (gfx950) backend for one HIP device.
 
-    def __init__(self, index: int = 0):
+    With no stream every op is synchronous (the result can be read at once,
+    as MatmulOps::matmul returns a value).  `set_stream(handle)` makes every
+    op asynchronous on that hipStream_t; device storage is then recycled in
+    that stream's order.
+    """
+
+    def __init__(self, index: int = 0, stream: int | None = None):
         self._device = Device.rocm(index)
+        self.stream = stream
+
+    def set_stream(self, stream: int | None) -> None:
+        self.stream = stream or None
+
+    def _s(self, stream):
+        s = stream if stream is not None else self.stream
+        return C.c_void_p(s) if s else None
 
     def device(self) -> Device:
         return self._device
@@ -57,7 +71,7 @@ class HipBackend:
                                   int(bias.dtype) if bias is not None else 0, int(act),
                                   C.c_void_p(aux.data_ptr() if aux is not None else 0))
         check(_lib.lib().oxm_gemm(C.byref(a), C.byref(b), C.byref(c), C.byref(ep) if ep is not None else None,
-                                  C.c_void_p(stream) if stream else None))
+                                  self._s(stream)))
         return out
 
     # ---- ReduceOps ----
@@ -67,7 +81,7 @@ class HipBackend:
                                    "(hip backend: rank-2, axis 0)")
         out = Tensor.empty((a.shape[1],), DType.F32, a.device)
         x, o = a.abi_view(), out.abi_view()
-        check(_lib.lib().oxm_sum_rows(C.byref(x), C.byref(o), C.c_void_p(stream) if stream else None))
+        check(_lib.lib().oxm_sum_rows(C.byref(x), C.byref(o), self._s(stream)))
         return out
 
     def max(self, a: Tensor, axes: Sequence[int]) -> Tensor:
@@ -99,7 +113,7 @@ class HipBackend:
         dy = Tensor.empty(y.shape, y.dtype, y.device)
         vy, vt, vl, vd = y.abi_view(), t.abi_view(), loss.abi_view(), dy.abi_view()
         check(_lib.lib().oxm_mse_loss_grad(C.byref(vy), C.byref(vt), C.byref(vl), C.byref(vd),
-                                           C.c_void_p(stream) if stream else None))
+                                           self._s(stream)))
         return loss, dy
 
 

@@ -13,6 +13,7 @@ hipError_t launch_gemm_f16(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipSt
 TileShape tile_shape(int cfg) {
     switch (cfg) {
     case kCfgH_256:
+    case kCfgH_256_4W:
     case kCfgH_256_NS: return {256, 256};
     case kCfgH_128: return {128, 128};
     default: return {128, 128};

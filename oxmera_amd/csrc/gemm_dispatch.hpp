@@ -13,14 +13,22 @@ hipError_t launch_one(const GemmArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Direct-to-LDS kernel (16-bit, both operands K-contiguous).
-template <typename T, int BM, int BN, int WM, int WN, int NS>
+// Direct-to-LDS kernel (16-bit operands, each K- or M/N-contiguous).
+template <typename T, int BM, int BN, int WM, int WN, int NS, int BKS, bool AMN, bool BMN>
 hipError_t launch_dl(GemmArgs a, hipStream_t s) {
     a.group_m = 4;
     int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n * a.batch;
     dim3 grid((unsigned)ntiles), block(WM * WN * 64);
-    hipLaunchKernelGGL((gemm_kernel_dl<T, BM, BN, WM, WN, NS>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((gemm_kernel_dl<T, BM, BN, WM, WN, NS, BKS, AMN, BMN>), grid, block, 0, s, a);
     return hipGetLastError();
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int NS, int BKS>
+hipError_t pick_dl(const GemmArgs &a, int la, int lb, hipStream_t s) {
+    if (la == kLdK && lb == kLdK) return launch_dl<T, BM, BN, WM, WN, NS, BKS, false, false>(a, s);
+    if (la == kLdK) return launch_dl<T, BM, BN, WM, WN, NS, BKS, false, true>(a, s);
+    if (lb == kLdK) return launch_dl<T, BM, BN, WM, WN, NS, BKS, true, false>(a, s);
+    return launch_dl<T, BM, BN, WM, WN, NS, BKS, true, true>(a, s);
 }
 
 template <typename T, int BM, int BN, int WM, int WN, Ld LA>

@@ -4,11 +4,11 @@
 namespace oxm {
 
 hipError_t launch_gemm_f16(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipStream_t s) {
-    if (ld_a == kLdK && ld_b == kLdK) {
-        // both operands K-contiguous: direct-to-LDS ring
-        if (cfg == kCfgH_128) return launch_dl<f16_t, 128, 128, 2, 2, 4>(a, s);
-        if (cfg == kCfgH_256_NS) return launch_one<f16_t, 256, 256, 2, 4, Ld::K, Ld::K>(a, s);
-        return launch_dl<f16_t, 256, 256, 2, 4, 4>(a, s);
+    if (ld_a != kLdG && ld_b != kLdG && cfg != kCfgH_256_NS) {
+        // K- or M/N-contiguous operands: direct-to-LDS ring
+        if (cfg == kCfgH_128) return pick_dl<f16_t, 128, 128, 2, 2, 2, 64>(a, ld_a, ld_b, s);
+        if (cfg == kCfgH_256_4W) return pick_dl<f16_t, 256, 256, 2, 2, 2, 64>(a, ld_a, ld_b, s);
+        return pick_dl<f16_t, 256, 256, 2, 4, 2, 64>(a, ld_a, ld_b, s);
     }
     if (cfg == kCfgH_128) return pick_a<f16_t, 128, 128, 2, 2>(a, ld_a, ld_b, s);
     return pick_a<f16_t, 256, 256, 2, 2>(a, ld_a, ld_b, s);

@@ -650,55 +650,98 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
 // while one is consumed.  One barrier per stage.
 // ===========================================================================
 
-// LDS layout of a stage: 64-byte rows (32 k of a 16-bit type, four 16-byte
-// chunks), four rows per 256-byte line.  Position of chunk c of row r in its
-// line: (r % 4) * 4 + (c ^ ((r / 4) % 4)).  A fragment read (16 consecutive
-// rows, one chunk) covers all 16 positions of the 256-byte bank width.
+// K-major stage layout (operand K-contiguous in HBM): 64-byte rows (32 k of
+// a 16-bit type, four 16-byte chunks), four rows per 256-byte line; chunk c
+// of row r sits at position (r % 4) * 4 + (c ^ ((r / 4) % 4)) of its line.  A
+// fragment read (16 consecutive rows, one chunk) covers all 16 positions of
+// the 256-byte bank width.
 __device__ __forceinline__ uint32_t lds_off64(int r, int c) {
     return (uint32_t)((r >> 2) * 256 + (((r & 3) << 2) | (c ^ ((r >> 2) & 3))) * 16);
+}
+
+// M/N-major stage layout (operand M/N-contiguous in HBM): one row of ROWS
+// elements per k (32 rows), in 64-byte segments; segment s of k-row r is
+// stored at segment s ^ (r % 4).  The DMA copies k-rows as they lie in HBM;
+// fragments are formed with transposing reads (ds_read_b64_tr_b16).
+template <int ROWS>
+__device__ __forceinline__ uint32_t lds_off_mn(int r, int byte_in_row) {
+    return (uint32_t)(r * ROWS * 2 + ((((byte_in_row >> 6) ^ (r & 3)) << 6) | (byte_in_row & 63)));
 }
 
 // s_waitcnt immediate that waits for vmcnt <= n and nothing else (gfx9
 // encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
 constexpr int waitcnt_vm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
 
-// One operand tile of ROWS rows: each wave instruction fills one 1 KB block
-// (16 rows x 64 B) of the stage; lane L of block b reads row
-// 16 b + 4 (L / 16) + (L % 16) / 4, chunk (L % 4) ^ (L / 16).
-template <int ROWS, int NT>
+// Global -> LDS DMA of one operand tile (ROWS rows of M or N, BKS k) per
+// stage.  Each wave instruction fills one 1 KB block; every lane fetches the
+// 16 bytes that belong at its position (lane L writes block byte 16 L), so
+// the stage layout is produced by the choice of global addresses.  With
+// BKS = 64 a K-major row is 128 bytes and every row is one 128-byte request
+// (BKS = 32 halves the bytes per L2 request).
+template <int ROWS, int NT, bool MN, int BKS>
 struct DirectLoader {
     static constexpr int kWaves = NT / 64;
-    static constexpr int kBlocks = ROWS / 16;
+    static constexpr int kBlocks = ROWS * BKS * 2 / 1024;
     static constexpr int kPer = kBlocks / kWaves;  // load instructions per wave per stage
     static_assert(kBlocks % kWaves == 0, "blocks must divide among the waves");
+    static_assert(BKS == 32 || BKS == 64, "32 or 64 k per stage");
     const char *base;
-    int64_t nbytes, K;
+    int64_t nbytes, K, sk_bytes;
     uint32_t voff[kPer];
-    int chunk;
+    int krow[kPer];  // M/N-major: the k-row each lane fills
+    int chunk;       // K-major: the k-chunk each lane fills
 
-    __device__ __forceinline__ DirectLoader(const char *b, int64_t s_mn, int64_t rows_left, int64_t k, int wave,
-                                            int lane)
+    __device__ __forceinline__ DirectLoader(const char *b, int64_t s_mn, int64_t s_k, int64_t rows_left, int64_t k,
+                                            int wave, int lane)
         : base(b), K(k) {
-        const int line = lane >> 4, pos = lane & 15;
-        chunk = (pos & 3) ^ line;
         const int64_t rows_here = rows_left < ROWS ? rows_left : ROWS;
-        nbytes = ((rows_here - 1) * s_mn + k) * 2;
+        if constexpr (!MN) {
+            sk_bytes = 2;
+            nbytes = ((rows_here - 1) * s_mn + k) * 2;
+            const int line = lane >> 4, pos = lane & 15;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int blk = wave + i * kWaves;
-            const int r = blk * 16 + line * 4 + (pos >> 2);
-            voff[i] = r < rows_left ? (uint32_t)(r * s_mn * 2 + chunk * 16) : kOob;
+            for (int i = 0; i < kPer; ++i) {
+                const int blk = wave + i * kWaves;
+                int r;
+                if constexpr (BKS == 32) {
+                    // 16 rows x 64 B per block: row 16 b + 4 (L/16) + (L%16)/4, chunk (L%4) ^ (L/16)
+                    chunk = (pos & 3) ^ line;
+                    r = blk * 16 + line * 4 + (pos >> 2);
+                } else {
+                    // 8 rows x 128 B per block (inverse of lds_off): line sr = 4 b + L/16,
+                    // half h = (L%16)/8, position p = L%8
+                    const int sr = blk * 4 + line, h = pos >> 3, pc = pos & 7;
+                    r = 2 * sr + (h ^ ((sr >> 2) & 1));
+                    chunk = pc ^ (sr & 7);
+                }
+                voff[i] = r < rows_left ? (uint32_t)(r * s_mn * 2 + chunk * 16) : kOob;
+                krow[i] = 0;
+            }
+        } else {
+            // block b covers 1024 / (2 ROWS) k-rows; lane L's byte in the stage
+            // is 1024 b + 16 L
+            sk_bytes = s_k * 2;
+            chunk = 0;
+            nbytes = (k - 1) * sk_bytes + rows_here * 2;
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                const int blk = wave + i * kWaves;
+                const int pos = blk * 1024 + lane * 16;
+                const int r = pos / (ROWS * 2), bir = pos % (ROWS * 2);
+                const int mn = (((bir >> 6) ^ (r & 3)) << 5) + ((bir & 63) >> 1);
+                krow[i] = r;
+                voff[i] = mn < rows_left ? (uint32_t)(r * sk_bytes + mn * 2) : kOob;
+            }
         }
     }
-    // Issue the loads of K step kt (32 k) into the stage at `dst`.  Written
-    // as inline asm so the compiler does not treat the DMA as an LDS store
-    // it must wait for before every LDS read; the kernel orders it
-    // explicitly (s_waitcnt vmcnt + s_barrier).
+    // Issue the DMA of K step kt (BKS k) into the stage at `dst`.  Inline asm
+    // keeps the compiler from treating it as an LDS store it must drain before
+    // every LDS read; the kernel orders it explicitly (vmcnt + s_barrier).
     __device__ __forceinline__ void issue(uint8_t *dst, int kt, int wave) {
-        const int64_t k0 = (int64_t)kt * 32;
-        int64_t nb = nbytes - k0 * 2;
+        const int64_t k0 = (int64_t)kt * BKS;
+        int64_t nb = nbytes - k0 * sk_bytes;
         nb = nb < 0 ? 0 : (nb > (int64_t)kMaxRec ? (int64_t)kMaxRec : nb);
-        const uint64_t addr = (uint64_t)(base + k0 * 2);
+        const uint64_t addr = (uint64_t)(base + k0 * sk_bytes);
         i32x4_t rsrc;
         rsrc.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
         rsrc.y = __builtin_amdgcn_readfirstlane((int)(uint32_t)(addr >> 32) & 0xffff);
@@ -710,21 +753,84 @@ struct DirectLoader {
         for (int i = 0; i < kPer; ++i) {
             const int blk = wave + i * kWaves;
             const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_base + blk * 1024);
-            const uint32_t vo = k_ok ? voff[i] : kOob;
+            bool ok;
+            if constexpr (MN)
+                ok = k0 + krow[i] < K;
+            else
+                ok = k_ok;
+            const uint32_t vo = ok ? voff[i] : kOob;
             asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(vo), "s"(rsrc), "{m0}"(m0) : "memory");
         }
     }
 };
 
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int NS>
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+// MFMA fragments of one operand from a stage: TILES tiles of 32 rows
+// starting at row0, fragment g = k 16g .. 16g+15 (g < BKS/16).  Lane l
+// supplies row l % 32 and k 16g + 8 (l / 32) + 0..7, for A and B alike.
+template <int ROWS, int TILES, bool MN, int BKS>
+struct FragReader {
+    static constexpr int kG = BKS / 16;
+    static constexpr int kTileStride = BKS == 32 ? 2048 : 4096;  // K-major: bytes between tiles
+    uint32_t off[kG];           // K-major: per g
+    uint32_t rowpart[kG][2];    // M/N-major: per (g, t)
+    uint32_t seg[TILES];        // M/N-major: per tile
+
+    __device__ __forceinline__ FragReader(uint32_t region, int row0, int lane) {
+        if constexpr (!MN) {
+            const int half = lane >> 5;
+            const int r = row0 + (lane & 31);
+#pragma unroll
+            for (int g = 0; g < kG; ++g)
+                off[g] = region + (BKS == 32 ? lds_off64(r, 2 * g + half) : lds_off(r, 2 * g + half));
+        } else {
+            // ds_read_b64_tr_b16: in each 16-lane group, output lane 4a + b gets
+            // element b of the 8-byte blocks addressed by lanes a, a+4, a+8, a+12.
+            // Lane a + 4j addresses k-row k0 + j at columns mnb + 4a .. +3, so
+            // lane i of the group receives k0 .. k0+3 of column mnb + i.
+            const int grp = lane >> 4, h = grp >> 1, mnb = (grp & 1) * 16;
+            const int a = lane & 3, j = (lane >> 2) & 3;
+#pragma unroll
+            for (int g = 0; g < kG; ++g)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    rowpart[g][t] = region + (16 * g + 8 * h + 4 * t + j) * ROWS * 2 + (mnb + 4 * a) * 2;
+#pragma unroll
+            for (int i = 0; i < TILES; ++i) seg[i] = (uint32_t)((((row0 >> 5) + i) ^ j) << 6);
+        }
+    }
+    __device__ __forceinline__ void read(const uint8_t *stage, int g, uint4 (&out)[TILES]) const {
+#pragma unroll
+        for (int i = 0; i < TILES; ++i) {
+            if constexpr (!MN) {
+                out[i] = *(const uint4 *)(stage + off[g] + i * kTileStride);
+            } else {
+                typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+                const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_i16x4 *)(uintptr_t)(uint32_t)(uintptr_t)(stage + rowpart[g][0] + seg[i]));
+                const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_i16x4 *)(uintptr_t)(uint32_t)(uintptr_t)(stage + rowpart[g][1] + seg[i]));
+                const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+                out[i] = make_uint4(l2.x, l2.y, h2.x, h2.y);
+            }
+        }
+    }
+};
+
+// Direct-to-LDS GEMM for 16-bit operands that are K- or M/N-contiguous
+// (AMN / BMN: the operand is M/N-major).  NS stages of BKS k form a ring;
+// NS-1 stages are in flight while one is consumed; one barrier per stage.
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int NS, int BKS, bool AMN, bool BMN>
 __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dl(GemmArgs p) {
     constexpr int NT = WAVES_M * WAVES_N * 64;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int TM = WM / 32, TN = WN / 32;
-    constexpr int kStageA = BM * 64, kStageB = BN * 64;
+    constexpr int kStageA = BM * BKS * 2, kStageB = BN * BKS * 2;
     constexpr int kStage = kStageA + kStageB;
+    constexpr int kG = BKS / 16;
     static_assert(Elem<T>::kBytes == 2, "direct-to-LDS path is for 16-bit operands");
-    static_assert(NS >= 3, "at least three stages");
+    static_assert(NS >= 2, "at least two stages");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
 
     const int tid = threadIdx.x;
@@ -756,68 +862,77 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dl(GemmArgs
             offb += i * p.bsb[d];
         }
     }
-    DirectLoader<BM, NT> la((const char *)p.a + (offa + m0 * p.sam) * 2, p.sam, p.M - m0, p.K, wave, lane);
-    DirectLoader<BN, NT> lb((const char *)p.b + (offb + n0 * p.sbn) * 2, p.sbn, p.N - n0, p.K, wave, lane);
-    constexpr int kLoadsPerStage = DirectLoader<BM, NT>::kPer + DirectLoader<BN, NT>::kPer;
+    DirectLoader<BM, NT, AMN, BKS> la((const char *)p.a + (offa + m0 * p.sam) * 2, p.sam, p.sak, p.M - m0, p.K, wave, lane);
+    DirectLoader<BN, NT, BMN, BKS> lb((const char *)p.b + (offb + n0 * p.sbn) * 2, p.sbn, p.sbk, p.N - n0, p.K, wave, lane);
+    constexpr int kLoadsPerStage = DirectLoader<BM, NT, AMN, BKS>::kPer + DirectLoader<BN, NT, BMN, BKS>::kPer;
+    const FragReader<BM, TM, AMN, BKS> fra(0, wm * WM, lane);
+    const FragReader<BN, TN, BMN, BKS> frb(kStageA, wn * WN, lane);
 
     f32x16_t acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x16_t{};
-
-    // Fragment g (16 k) of a stage: lane l reads chunk 2g + l/32 of row
-    // base + l%32; rows 32 apart are 2048 bytes apart in this layout.
-    const int half = lane >> 5;
-    const int arow = wm * WM + (lane & 31);
-    const int brow = wn * WN + (lane & 31);
-    uint32_t aoff[2], boff[2];
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        aoff[g] = lds_off64(arow, 2 * g + half);
-        boff[g] = kStageA + lds_off64(brow, 2 * g + half);
-    }
     uint4 fa[2][TM], fb[2][TN];
-    auto read_frags = [&](const uint8_t *stage, int g, uint4(&A)[TM], uint4(&B)[TN]) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) A[i] = *(const uint4 *)(stage + aoff[g] + i * 2048);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) B[j] = *(const uint4 *)(stage + boff[g] + j * 2048);
-    };
 
-    const int nk = (int)((p.K + 31) / 32);
-    // Prologue: stages 0 .. NS-2 in flight.
+    const int nk = (int)((p.K + BKS - 1) / BKS);
+    // Software pipeline.  Step kt computes stage kt % NS while NS-1 later
+    // stages are in flight.  The MFMAs of the last fragment group of step kt
+    // use registers only, so they are issued AFTER the barrier, under the LDS
+    // latency of step kt+1's first fragment reads; before the barrier every
+    // LDS read of step kt has landed (lgkmcnt 0), which is what lets the DMA
+    // of step kt+NS overwrite stage kt % NS right after it.
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s) {
         la.issue(lds + s * kStage, s, wave);
         lb.issue(lds + s * kStage + kStageA, s, wave);
     }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * kLoadsPerStage));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    la.issue(lds + (NS - 1) * kStage, NS - 1, wave);
+    lb.issue(lds + (NS - 1) * kStage + kStageA, NS - 1, wave);
+    fra.read(lds, 0, fa[0]);
+    frb.read(lds, 0, fb[0]);
     int cur = 0;  // stage of step kt
     for (int kt = 0; kt < nk; ++kt) {
-        // Step kt's loads are the oldest NS-1 stages ago: wait for them, then
-        // the barrier makes every wave's part visible and frees stage kt-1.
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * kLoadsPerStage));
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-        int nxt = cur == 0 ? NS - 1 : cur - 1;  // (kt + NS - 1) % NS
-        la.issue(lds + nxt * kStage, kt + NS - 1, wave);
-        lb.issue(lds + nxt * kStage + kStageA, kt + NS - 1, wave);
         const uint8_t *stage = lds + cur * kStage;
-        read_frags(stage, 0, fa[0], fb[0]);
-        read_frags(stage, 1, fa[1], fb[1]);
-#pragma unroll
-        for (int g = 0; g < 2; ++g)
+        static_for<0, kG - 1>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            fra.read(stage, g + 1, fa[(g + 1) & 1]);
+            frb.read(stage, g + 1, fb[(g + 1) & 1]);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j) Mma<T>::run(acc[i][j], fa[g][i], fb[g][j]);
+                for (int j = 0; j < TN; ++j) Mma<T>::run(acc[i][j], fa[g & 1][i], fb[g & 1][j]);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        // every LDS read of step kt landed; this wave's DMA of step kt+1 landed
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * kLoadsPerStage) & ~(0xF << 8));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        la.issue(lds + cur * kStage, kt + NS, wave);
+        lb.issue(lds + cur * kStage + kStageA, kt + NS, wave);
+        __builtin_amdgcn_sched_barrier(0);
         cur = cur + 1 == NS ? 0 : cur + 1;
+        const uint8_t *next = lds + cur * kStage;
+        fra.read(next, 0, fa[0]);
+        frb.read(next, 0, fb[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        constexpr int gl = (kG - 1) & 1;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) Mma<T>::run(acc[i][j], fa[gl][i], fb[gl][j]);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    // Loads past the end of K were issued (out of range: they write zeros to
-    // LDS); drain them before the LDS is reused for the epilogue.
+    // DMA past the end of K was issued (out of range: it writes zeros to
+    // LDS); drain it before the LDS is reused for the epilogue.
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __syncthreads();
 
+    const int half = lane >> 5;
     constexpr int kSld = WN + 8;
     static_assert(NT / 64 * 32 * kSld * 4 <= NS * kStage, "epilogue staging must fit in LDS");
     float *ws = (float *)lds + wave * 32 * kSld;

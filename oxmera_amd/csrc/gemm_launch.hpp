@@ -12,11 +12,12 @@ enum LoaderKind : int { kLdK = 0, kLdMN = 1, kLdG = 2 };
 // Tile configurations.
 enum TileCfg : int {
     kCfgF32_128 = 0,   // f32: 128x128 tile, 2x2 waves of 64x64, BK 32
-    kCfgH_256 = 1,     // bf16/f16: 256x256 tile, 2x2 waves of 128x128, BK 64
+    kCfgH_256 = 1,     // bf16/f16: 256x256 tile, 2x4 waves of 128x64 (direct-to-LDS), BK 64
     kCfgH_128 = 2,     // bf16/f16: 128x128 tile, 2x2 waves of 64x64, BK 64
-                       // (K-contiguous A and B use the direct-to-LDS ring:
-                       //  256x256 = 2x4 waves, 4 stages of 32 k; 128x128 = 2x2 waves)
-    // tuning variant (16-bit, K-contiguous A and B; selected by OXM_GEMM_CFG)
+                       // (K- or M/N-contiguous operands use the direct-to-LDS kernel:
+                       //  2 stages of 64 k, 128-byte rows)
+    // tuning variants (16-bit; selected by OXM_GEMM_CFG)
+    kCfgH_256_4W = 3,  // direct-to-LDS 256x256 with 2x2 waves of 128x128
     kCfgH_256_NS = 4,  // 256x256 register-staged kernel instead of the direct-to-LDS one
 };
 

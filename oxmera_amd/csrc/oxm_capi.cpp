@@ -10,6 +10,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
 
 #include "../../include/oxm.h"
@@ -103,11 +105,48 @@ bool is_contiguous(const oxm_view *v) {
     return true;
 }
 
+// Allocations made through oxm_alloc: base -> (bytes, device).  Views over
+// them are validated against this registry without any HIP query (the HIP
+// pointer queries synchronise with the device, which would serialise
+// asynchronous launches); other pointers fall back to the HIP queries.
+struct AllocInfo {
+    size_t bytes;
+    int device;
+};
+std::mutex g_alloc_mu;
+std::map<uintptr_t, AllocInfo> g_allocs;
+
+// The registered allocation containing p, if any.
+bool find_alloc(const void *p, uintptr_t *base, AllocInfo *info) {
+    const uintptr_t a = (uintptr_t)p;
+    std::lock_guard<std::mutex> lock(g_alloc_mu);
+    auto it = g_allocs.upper_bound(a);
+    if (it == g_allocs.begin()) return false;
+    --it;
+    if (a >= it->first + it->second.bytes) return false;
+    *base = it->first;
+    *info = it->second;
+    return true;
+}
+
 // The device allocation holding [p, p + bytes) must contain it entirely and
 // live on `device`.  This is what keeps a malformed view from reaching the
 // GPU as an out-of-bounds access.
 oxm_status check_device_range(const void *p, int64_t lo_bytes, int64_t hi_bytes, int device, const char *what,
                               const char *op) {
+    uintptr_t rbase;
+    AllocInfo info;
+    if (find_alloc(p, &rbase, &info)) {
+        if (info.device != device)
+            return fail(OXM_E_DEVICE_MISMATCH, "%s: %s lives on %s, expected %s", op, what,
+                        device_str(info.device).c_str(), device_str(device).c_str());
+        const int64_t rel = (int64_t)((uintptr_t)p - rbase);
+        if (rel + lo_bytes < 0 || rel + hi_bytes > (int64_t)info.bytes)
+            return fail(OXM_E_INDEX_OUT_OF_BOUNDS,
+                        "%s: %s addresses bytes [%lld, %lld) relative to its pointer, outside its %zu-byte allocation",
+                        op, what, (long long)lo_bytes, (long long)hi_bytes, info.bytes);
+        return OXM_OK;
+    }
     hipPointerAttribute_t attr;
     memset(&attr, 0, sizeof attr);
     hipError_t e = hipPointerGetAttributes(&attr, p);
@@ -361,7 +400,7 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
         int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
         cfg = big_tiles >= 256 ? oxm::kCfgH_256 : oxm::kCfgH_128;
         cfg = env_int("OXM_GEMM_CFG", cfg);
-        if (cfg != oxm::kCfgH_256 && cfg != oxm::kCfgH_128 && cfg != oxm::kCfgH_256_NS) cfg = oxm::kCfgH_128;
+        if (cfg < oxm::kCfgH_256 || cfg > oxm::kCfgH_256_NS) cfg = oxm::kCfgH_128;
     }
     oxm::TileShape ts = oxm::tile_shape(cfg);
     int ld_a = classify((const char *)g.a, g.sam, g.sak, M, K, g.bsa, nbd, es, ts.bm);
@@ -454,11 +493,19 @@ oxm_status oxm_alloc(int32_t device, size_t bytes, void **out) {
         *out = nullptr;
         return hip_fail(e, "alloc");
     }
+    {
+        std::lock_guard<std::mutex> lock(g_alloc_mu);
+        g_allocs[(uintptr_t)*out] = AllocInfo{bytes ? bytes : 1, device};
+    }
     return ok();
 }
 
 oxm_status oxm_free(int32_t device, void *ptr) {
     if (!ptr) return ok();
+    {
+        std::lock_guard<std::mutex> lock(g_alloc_mu);
+        g_allocs.erase((uintptr_t)ptr);
+    }
     DeviceGuard guard(device < 0 ? 0 : device);
     hipError_t e = hipFree(ptr);
     if (e != hipSuccess) return hip_fail(e, "free");

@@ -45,8 +45,62 @@ def _np_dtype(dt: DType):
 # ---- storage -------------------------------------------------------------------
 
 
+class _DevicePool:
+    """Caching allocator for device storage (one per device).
+
+    Freed blocks are kept per exact byte size and handed out again instead of
+    calling hipFree (which synchronises the device).  Reuse is safe for work
+    issued in stream order on one stream -- the backend's -- like PyTorch's
+    caching allocator; `release()` returns everything to HIP.
+    """
+
+    def __init__(self, device: int, cap_bytes: int = 64 << 30):
+        self.device = device
+        self.cap = cap_bytes
+        self.free: dict[int, list[int]] = {}
+        self.cached = 0
+
+    def get(self, nbytes: int) -> int:
+        lst = self.free.get(nbytes)
+        if lst:
+            self.cached -= nbytes
+            return lst.pop()
+        p = C.c_void_p()
+        st = _lib.lib().oxm_alloc(self.device, nbytes, C.byref(p))
+        if st != _lib.OK:  # out of memory: give the cache back and retry once
+            self.release()
+            st = _lib.lib().oxm_alloc(self.device, nbytes, C.byref(p))
+        check(st)
+        return p.value
+
+    def put(self, ptr: int, nbytes: int) -> None:
+        if self.cached + nbytes > self.cap:
+            _lib.lib().oxm_free(self.device, C.c_void_p(ptr))
+            return
+        self.free.setdefault(nbytes, []).append(ptr)
+        self.cached += nbytes
+
+    def release(self) -> None:
+        for lst in self.free.values():
+            for ptr in lst:
+                _lib.lib().oxm_free(self.device, C.c_void_p(ptr))
+        self.free.clear()
+        self.cached = 0
+
+
+_POOLS: dict[int, _DevicePool] = {}
+
+
+def device_pool(index: int) -> _DevicePool:
+    pool = _POOLS.get(index)
+    if pool is None:
+        pool = _POOLS[index] = _DevicePool(index)
+    return pool
+
+
 class Storage:
-    """A byte buffer on one device; host storage wraps a numpy byte array."""
+    """A byte buffer on one device; host storage wraps a numpy byte array,
+    device storage is a block of the device's caching allocator."""
 
     def __init__(self, nbytes: int, dtype: DType, device: Device):
         self.nbytes = int(nbytes)
@@ -57,9 +111,7 @@ class Storage:
         if device.kind == "cpu":
             self._host = np.zeros(max(1, self.nbytes), dtype=np.uint8)
         else:
-            p = C.c_void_p()
-            check(_lib.lib().oxm_alloc(device.index, self.nbytes, C.byref(p)))
-            self._ptr = p.value
+            self._ptr = device_pool(device.index).get(max(1, self.nbytes))
 
     @property
     def ptr(self) -> int:
@@ -70,7 +122,7 @@ class Storage:
     def __del__(self):
         if getattr(self, "_ptr", None):
             try:
-                _lib.lib().oxm_free(self.device.index, C.c_void_p(self._ptr))
+                device_pool(self.device.index).put(self._ptr, max(1, self.nbytes))
             except Exception:
                 pass
             self._ptr = None
