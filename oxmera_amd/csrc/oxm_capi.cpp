@@ -515,6 +515,10 @@ oxm_status oxm_free(int32_t device, void *ptr) {
 oxm_status oxm_copy(void *dst, int32_t dst_device, const void *src, int32_t src_device, size_t bytes, void *stream) {
     if (bytes == 0) return ok();
     if (!dst || !src) return fail(OXM_E_INVALID_ARGUMENT, "copy: NULL pointer");
+    if (dst_device < 0 && src_device < 0) {  // host to host needs no device
+        memmove(dst, src, bytes);
+        return ok();
+    }
     hipMemcpyKind kind;
     if (dst_device < 0 && src_device < 0)
         kind = hipMemcpyHostToHost;
