@@ -94,7 +94,10 @@ def make_operand(dtype, kind, rows, cols, seed, which):
 
 
 LAYOUTS = ["row", "col", "gather", "flip", "colgap"]
-SHAPES = [(64, 128, 64), (70, 136, 90), (300, 64, 260), (33, 200, 17), (257, 96, 129)]
+# (64,200,72) and (136,72,200): every extent a multiple of 8 with K not a
+# multiple of 64, so the M/N-major direct-to-LDS path runs with a K tail.
+SHAPES = [(64, 128, 64), (70, 136, 90), (300, 64, 260), (33, 200, 17), (257, 96, 129), (64, 200, 72),
+          (136, 72, 200)]
 
 
 @pytest.mark.parametrize("dtype", [F32, BF16, F16], ids=["f32", "bf16", "f16"])
@@ -121,6 +124,22 @@ def test_batched_broadcast_small(hip, dtype):
     c = hip.matmul(a.dev, b.dev)
     assert c.shape == (3, 2, 37, 45)
     assert_close(to_f32(c), O.matmul(a.ora, b.ora), spec_tolerance(dtype, 40), "batched")
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "f16"])
+def test_batched_direct_to_lds(hip, dtype):
+    """Batched 16-bit GEMM whose operands both qualify for the direct-to-LDS
+    path: A M-contiguous (a transposed view per batch), B K-contiguous, B
+    broadcast over the batch, K with a tail."""
+    rng = np.random.default_rng(5)
+    nb, m, k, n = 3, 96, 328, 136
+    abuf = host_buffer(dtype, rng.uniform(-1, 1, nb * k * m).astype(np.float32))
+    a = Operand(dtype, abuf, (nb, m, k), (k * m, 1, m))          # per batch: [m, k] with stride_m = 1
+    bbuf = host_buffer(dtype, rng.uniform(-1, 1, n * k).astype(np.float32))
+    b = Operand(dtype, bbuf, (1, k, n), (n * k, 1, k))           # [1, k, n], K-contiguous
+    c = hip.matmul(a.dev, b.dev)
+    assert c.shape == (nb, m, n)
+    assert_close(to_f32(c), O.matmul(a.ora, b.ora), spec_tolerance(dtype, k), "batched direct-to-LDS")
 
 
 def test_zero_sized_and_k_zero(hip):
