@@ -174,7 +174,7 @@ def cpu_baseline(kind: str, host, desc, budget_s: float = 12.0):
 
 
 def kernel_name(kind: str) -> str:
-    return ("gemm_kernel<float,128,128,2,2,Ld::K,Ld::MN> (register-staged LDS double buffer)" if kind == "f32"
+    return ("gemm_kernel<float,256,256,2,4,Ld::K,Ld::MN> (register-staged LDS double buffer, 8 waves)" if kind == "f32"
             else "gemm_kernel_dl<bf16_t,256,256,2,4,2,64> (direct-to-LDS, 2 stages of 64 k, 8 waves)")
 
 

@@ -14,7 +14,8 @@ TileShape tile_shape(int cfg) {
     switch (cfg) {
     case kCfgH_256:
     case kCfgH_256_4W:
-    case kCfgH_256_NS: return {256, 256};
+    case kCfgH_256_NS:
+    case kCfgF32_256: return {256, 256};
     case kCfgH_128: return {128, 128};
     default: return {128, 128};
     }

@@ -19,6 +19,7 @@ enum TileCfg : int {
     // tuning variants (16-bit; selected by OXM_GEMM_CFG)
     kCfgH_256_4W = 3,  // direct-to-LDS 256x256 with 2x2 waves of 128x128
     kCfgH_256_NS = 4,  // 256x256 register-staged kernel instead of the direct-to-LDS one
+    kCfgF32_256 = 5,   // f32: 256x256 tile, 2x4 waves of 128x64, BK 32 (problems of >= 256 tiles)
 };
 
 struct TileShape {

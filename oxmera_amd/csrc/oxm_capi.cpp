@@ -394,10 +394,13 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     g.bias_dtype = ep->bias_dtype;
 
     int cfg;
+    const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
     if (a->dtype == OXM_F32) {
-        cfg = oxm::kCfgF32_128;
+        // 256x256 tiles once they fill the 256 CUs, 128x128 below that
+        cfg = big_tiles >= 256 ? oxm::kCfgF32_256 : oxm::kCfgF32_128;
+        cfg = env_int("OXM_GEMM_CFG_F32", cfg);
+        if (cfg != oxm::kCfgF32_256) cfg = oxm::kCfgF32_128;
     } else {
-        int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
         cfg = big_tiles >= 256 ? oxm::kCfgH_256 : oxm::kCfgH_128;
         cfg = env_int("OXM_GEMM_CFG", cfg);
         if (cfg < oxm::kCfgH_256 || cfg > oxm::kCfgH_256_NS) cfg = oxm::kCfgH_128;
