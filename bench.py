@@ -10,13 +10,14 @@ A "step" is one GEMM launch over inputs already resident in HBM.
                     N(0, 0.02)                                  -> "extra"
 
 Timing: W untimed warm-up launches, then K launches bracketed by HIP events
-on the stream the kernel runs on (torch's current stream, handed to
-oxm_gemm), with device synchronisation on both sides.  The roofline figure
+on the stream the kernel runs on (a dedicated non-default stream handed to
+oxm_gemm, so launches are asynchronous), with device synchronisation on
+both sides.  The roofline figure
 is algorithmic flops per launch / average launch time against the dense
 MFMA peak of the dtype.  cpu_baseline times the naive CPU oracle on a
 bounded sample of output rows on this host and extrapolates.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload f32|bf16]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload f32|bf16|mlp]
 """
 from __future__ import annotations
 
@@ -212,7 +213,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", choices=["f32", "bf16", "mlp"], default="f32",
                     help="f32 / bf16 time one GEMM; mlp times the MLP step alone (for profiling)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the extra workload")
