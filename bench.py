@@ -9,7 +9,8 @@ A "step" is one GEMM launch over inputs already resident in HBM.
                     B a transposed strided view (strides [1, 8192]),
                     N(0, 0.02)                                  -> "extra"
 
-Timing: W untimed warm-up launches, then K launches bracketed by HIP events
+Timing: W untimed warm-up launches (and at least 0.3 s of them), then K
+launches bracketed by HIP events
 on the stream the kernel runs on (a dedicated non-default stream handed to
 oxm_gemm, so launches are asynchronous), with device synchronisation on
 both sides.  The roofline figure
@@ -34,33 +35,77 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK = {"f32": 157.3, "bf16": 2516.6}  # TFLOP/s, dense MFMA, MI355X (256 CU x 2.4 GHz)
+WARMUP_S = 0.3  # minimum warm-up time per workload (s)
+
+
+def _rng(seed: int):
+    return np.random.default_rng(seed)
 
 
 def make_inputs(kind: str):
+    """Device operands, an output tensor, the host buffers the CPU oracle
+    reads (buffer, oracle dtype, shape, strides per operand) and a config
+    description, for one BASELINE configuration:
+      f32    configs[1] C2: 4096^3, row-major, N(0,1)
+      bf16   configs[2] C3: 8192^3, B a transposed view, N(0,0.02)
+      c1     configs[0] C1: 256^3 f32, U[-1,1)
+      c2odd  configs[1] C2-odd: 4097x4093 . 4093x4095 f32 (row strides not 16-byte multiples), N(0,1)
+      c4     configs[3] C4: A [32,512,1024] = every other row of a [32,1024,1024]
+             buffer, B [1,1024,768] broadcast over the batch, U[-1,1)"""
     import oxmera_amd as ox
+    from oracle import oracle as O
     dev = ox.Device.rocm(0)
-    if kind == "f32":
-        m = k = n = 4096
-        rng = np.random.default_rng(12345)
-        a_h = rng.standard_normal((m, k), dtype=np.float32)
-        b_h = rng.standard_normal((k, n), dtype=np.float32)
+    if kind in ("f32", "c1", "c2odd"):
+        m, k, n, seed = {"f32": (4096, 4096, 4096, 12345), "c1": (256, 256, 256, 111),
+                         "c2odd": (4097, 4093, 4095, 2222)}[kind]
+        rng = _rng(seed)
+        if kind == "c1":
+            a_h = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+            b_h = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+        else:
+            a_h = rng.standard_normal((m, k), dtype=np.float32)
+            b_h = rng.standard_normal((k, n), dtype=np.float32)
         a = ox.Tensor.from_numpy(a_h, dev, ox.DType.F32)
         b = ox.Tensor.from_numpy(b_h, dev, ox.DType.F32)
-        host = (a_h, b_h)
-        desc = {"workload": "f32 matmul 4096x4096x4096, A and B contiguous row-major (BASELINE configs[1])",
-                "M": m, "N": n, "K": k, "a_strides": [k, 1], "b_strides": [n, 1], "seed": 12345}
-    else:
+        host = ((a_h, O.F32, (m, k), (k, 1)), (b_h, O.F32, (k, n), (n, 1)))
+        name = {"f32": "f32 matmul 4096x4096x4096, A and B contiguous row-major (BASELINE configs[1])",
+                "c1": "f32 matmul 256x256x256, contiguous, U[-1,1) (BASELINE configs[0])",
+                "c2odd": "f32 matmul 4097x4093 . 4093x4095, contiguous, N(0,1) (BASELINE configs[1], odd shape)"}[kind]
+        desc = {"workload": name, "M": m, "N": n, "K": k, "batch": 1, "a_strides": [k, 1], "b_strides": [n, 1],
+                "seed": seed}
+        oshape = (m, n)
+    elif kind == "bf16":
         m = k = n = 8192
-        rng = np.random.default_rng(54321)
+        rng = _rng(54321)
         a_h = ox.f32_to_bf16_bits(rng.normal(0, 0.02, (m, k)).astype(np.float32))
         bbuf = ox.f32_to_bf16_bits(rng.normal(0, 0.02, (n, k)).astype(np.float32))
         a = ox.Tensor.from_numpy(a_h, dev, ox.DType.BF16)
         b = ox.Tensor.from_numpy(bbuf, dev, ox.DType.BF16).permute([1, 0])  # [K, N], strides [1, K]
-        host = (a_h, bbuf)
+        host = ((a_h, O.BF16, (m, k), (k, 1)), (bbuf, O.BF16, (k, n), (1, k)))
         desc = {"workload": "bf16-in f32-out matmul 8192^3, A row-major, B transposed view strides [1,8192] "
                             "(BASELINE configs[2])",
-                "M": m, "N": n, "K": k, "a_strides": [k, 1], "b_strides": [1, k], "seed": 54321}
-    out = ox.Tensor.empty((m, n), ox.DType.F32, dev)
+                "M": m, "N": n, "K": k, "batch": 1, "a_strides": [k, 1], "b_strides": [1, k], "seed": 54321}
+        oshape = (m, n)
+    elif kind == "c4":
+        bt, m, k, n = 32, 512, 1024, 768
+        rng = _rng(4444)
+        abuf = rng.uniform(-1, 1, (bt, 2 * m, k)).astype(np.float32)
+        b_h = rng.uniform(-1, 1, (1, k, n)).astype(np.float32)
+        full = ox.Tensor.from_numpy(abuf, dev, ox.DType.F32)
+        a = full.with_layout((bt, m, k), (2 * m * k, 2 * k, 1), 0)  # every other row, no copy
+        b = ox.Tensor.from_numpy(b_h, dev, ox.DType.F32)
+        host = ((abuf, O.F32, (bt, m, k), (2 * m * k, 2 * k, 1)), (b_h, O.F32, (1, k, n), (k * n, n, 1)))
+        desc = {"workload": "batched f32 matmul: A [32,512,1024] every other row of a [32,1024,1024] buffer "
+                            "(strides [1048576,2048,1]), B [1,1024,768] broadcast, U[-1,1) (BASELINE configs[3])",
+                "M": m, "N": n, "K": k, "batch": bt, "a_strides": [2 * m * k, 2 * k, 1],
+                "b_strides": [k * n, n, 1], "seed": 4444}
+        oshape = (bt, m, n)
+    else:
+        raise ValueError(kind)
+    out = ox.Tensor.empty(oshape, ox.DType.F32, dev)
+    ws = sum(h[0].nbytes for h in host) + out.storage.nbytes
+    desc["working_set_bytes"] = int(ws)
+    desc["exceeds_256MB_infinity_cache"] = bool(ws > 256 * 2 ** 20)
     return a, b, out, host, desc
 
 
@@ -76,8 +121,14 @@ def time_gpu(kind: str, steps: int, warmup: int):
     ts = torch.cuda.Stream()
     stream = ts.cuda_stream
     with torch.cuda.stream(ts):
-        for _ in range(warmup):
+        # W launches, and at least WARMUP_S seconds of them: after an idle
+        # stretch (the CPU baseline) the clock takes a while to ramp up.
+        t0, n = time.perf_counter(), 0
+        while n < warmup or time.perf_counter() - t0 < WARMUP_S:
             be.matmul(a, b, out=out, stream=stream)
+            n += 1
+            if n % 8 == 0:
+                torch.cuda.synchronize()
         torch.cuda.synchronize()
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(ts)
@@ -96,7 +147,7 @@ def time_gpu(kind: str, steps: int, warmup: int):
             per.append((s, e))
         torch.cuda.synchronize()
     per_ms = sorted(s.elapsed_time(e) for s, e in per)
-    flops = 2.0 * desc["M"] * desc["N"] * desc["K"]
+    flops = 2.0 * desc["batch"] * desc["M"] * desc["N"] * desc["K"]
     return dict(total_ms=total_ms, per_ms=per_ms, flops=flops, desc=desc, host=host, out=out, a=a, b=b)
 
 
@@ -125,9 +176,11 @@ def time_mlp(steps: int, warmup: int):
     be.set_stream(stream.cuda_stream)
     try:
         with torch.cuda.stream(stream):
-            for _ in range(warmup):
+            t0, n = time.perf_counter(), 0
+            while n < warmup or time.perf_counter() - t0 < WARMUP_S:
                 model.train_step(x, t)
-            torch.cuda.synchronize()
+                n += 1
+                torch.cuda.synchronize()
             start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record(stream)
             for _ in range(steps):
@@ -146,37 +199,101 @@ def time_mlp(steps: int, warmup: int):
             "loss": float(loss.t.to_numpy()[0])}
 
 
-def cpu_baseline(kind: str, host, desc, budget_s: float = 12.0):
-    """The naive oracle on a bounded sample of output rows, all host threads."""
+def host_cpu() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _views(host):
+    from oracle import oracle as O
+    (ab, adt, ash, ast), (bb, bdt, bsh, bst) = host
+    return (O.StridedView(ab.reshape(-1), adt, ash, ast, 0), O.StridedView(bb.reshape(-1), bdt, bsh, bst, 0))
+
+
+def cpu_baseline(kind: str, host, desc, budget_s: float = 30.0):
+    """The naive oracle (oracle/oxm_oracle.c, one output row per task) on
+    the host cores: the whole output when that fits the budget, otherwise
+    a bounded random sample of output rows, extrapolated and labelled so."""
     from oracle import oracle as O
     threads = min(os.cpu_count() or 1, 16)
-    a_h, b_h = host
-    M, N, K = desc["M"], desc["N"], desc["K"]
-    if kind == "f32":
-        av = O.StridedView.contiguous(a_h)
-        bv = O.StridedView.contiguous(b_h)
-    else:
-        av = O.StridedView(a_h.reshape(-1), O.BF16, (M, K), (K, 1), 0)
-        bv = O.StridedView(b_h.reshape(-1), O.BF16, (K, N), (1, K), 0)
+    av, bv = _views(host)
+    rows_total = desc["batch"] * desc["M"]
+    N, K = desc["N"], desc["K"]
     rows = threads
     while True:
-        sel = np.random.default_rng(7).choice(M, size=rows, replace=False).astype(np.int64)
+        sel = np.sort(np.random.default_rng(7).choice(rows_total, size=rows, replace=False)).astype(np.int64)
         t0 = time.perf_counter()
         res = O.matmul(av, bv, rows=sel, nthreads=threads)
         dt = time.perf_counter() - t0
-        if dt >= budget_s / 4 or rows >= M:
+        if rows >= rows_total or dt >= budget_s / 8:
             break
-        rows = min(M, rows * max(2, int(budget_s / 4 / max(dt, 1e-3))))
+        est_full = dt * rows_total / rows
+        rows = rows_total if est_full <= budget_s * 0.6 else min(rows_total, rows * max(2, int(budget_s / 8 / max(dt, 1e-3))))
     tflops = 2.0 * rows * N * K / dt / 1e12
+    full = rows == rows_total
+    what = (f"all {rows_total} output rows" if full else
+            f"{rows} of {rows_total} output rows, extrapolated full time {dt * rows_total / rows:.1f} s")
     return {"value": tflops, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{rows} of {M} output rows ({rows * N} outputs, K={K}) in {dt:.2f} s by the naive "
-                      f"oxmera-cpu-style oracle (oracle/oxm_oracle.c, -O2, f32 ascending-k), "
-                      f"extrapolated full time {dt * M / rows:.0f} s"}, (sel, res)
+            "sample": f"{what} ({rows * N} outputs, K={K}) in {dt:.2f} s by the naive oxmera-cpu-style oracle "
+                      f"(oracle/oxm_oracle.c, -O2, f32 ascending-k, threaded over rows)",
+            "host_cpu": host_cpu(), "host_threads": os.cpu_count()}, (sel, res)
+
+
+def _abs_product(host, sel, desc):
+    """sum_k |a_ik| |b_kj| for the selected flattened rows (float32 is ample
+    for an error denominator)."""
+    from oracle import oracle as O
+    (ab, adt, ash, ast), (bb, bdt, bsh, bst) = host
+
+    def dense_abs(buf, dt, shape, strides):
+        arr = np.lib.stride_tricks.as_strided(buf.reshape(-1), shape=shape,
+                                              strides=[st * buf.itemsize for st in strides])
+        return np.abs(O.bf16_to_f32(np.ascontiguousarray(arr)) if dt == O.BF16 else arr.astype(np.float32))
+
+    M = desc["M"]
+    A = dense_abs(ab, adt, ash, ast).reshape(-1, desc["K"])
+    B = dense_abs(bb, bdt, bsh, bst)
+    if B.ndim == 2:
+        return (A[sel] @ B).astype(np.float64)
+    out = np.empty((len(sel), desc["N"]), np.float64)
+    for bi in np.unique(sel // M):
+        pick = np.nonzero(sel // M == bi)[0]
+        out[pick] = A[sel[pick]] @ B[0 if B.shape[0] == 1 else bi]
+    return out
+
+
+def spot_check(kind: str, res, sample, host=None, comp_rows: int = 64):
+    """Parity of the timed output against the oracle on its rows, with the
+    |c - r| <= tol * max(|r|, rms(r)), tol = 1e-5*sqrt(K)
+    (f32) or 1e-2 (bf16).  Also the componentwise error |c - r| / sum_k |a||b|
+    on up to comp_rows of those rows."""
+    sel, ref = sample
+    out = res["out"].to_numpy().reshape(-1, res["desc"]["N"])
+    got = out[sel].astype(np.float64)
+    ref = ref.astype(np.float64)
+    rms = float(np.sqrt(np.mean(ref * ref))) or 1e-30
+    tol = 1e-5 * np.sqrt(res["desc"]["K"]) if kind != "bf16" else 1e-2
+    worst = float(np.max(np.abs(got - ref) / (tol * np.maximum(np.abs(ref), rms))))
+    d = {"rows": int(len(sel)), "tol": float(tol), "max_err_over_tol": round(worst, 4), "pass": worst <= 1.0}
+    if host is not None:
+        idx = np.arange(len(sel)) if len(sel) <= comp_rows else np.linspace(0, len(sel) - 1, comp_rows).astype(int)
+        denom = _abs_product(host, sel[idx], res["desc"])
+        comp = np.abs(got[idx] - ref[idx]) / np.maximum(denom, 1e-30)
+        d["max_componentwise_err"] = float(np.max(comp))
+    return d
 
 
 def kernel_name(kind: str) -> str:
-    return ("gemm_kernel<float,256,256,2,4,Ld::K,Ld::MN> (register-staged LDS double buffer, 8 waves)" if kind == "f32"
-            else "gemm_kernel_dl<bf16_t,256,256,2,4,2,64> (direct-to-LDS, 2 stages of 64 k, 8 waves)")
+    if kind == "bf16":
+        return "gemm_kernel_dl<bf16_t,256,256,2,4,2,64> (direct-to-LDS, 2 stages of 64 k, 8 waves)"
+    if kind == "f32":
+        return "gemm_kernel<float,256,256,2,4,Ld::K,Ld::MN> (register-staged LDS double buffer, 8 waves)"
+    return "gemm_kernel<float,...> (register-staged; tile chosen by the dispatcher)"
 
 
 def traffic_for(kind: str):
@@ -193,20 +310,39 @@ def traffic_for(kind: str):
 def roofline(kind: str, res):
     avg_ms = res["total_ms"] / res["steps"]
     achieved = res["flops"] / (avg_ms * 1e-3) / 1e12
-    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK[kind], "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK[kind], 4), "traffic": traffic_for(kind),
+    peak = PEAK["bf16" if kind == "bf16" else "f32"]
+    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4), "traffic": traffic_for(kind) if kind in ("f32", "bf16") else None,
             "kernel": kernel_name(kind), "avg_launch_ms": round(avg_ms, 4)}
 
 
-def spot_check(kind: str, res, sample):
-    """Parity of the timed output on the CPU-baseline rows."""
-    sel, ref = sample
-    got = res["out"].to_numpy()[sel].astype(np.float64)
-    ref = ref.astype(np.float64)
-    rms = float(np.sqrt(np.mean(ref * ref))) or 1e-30
-    tol = 1e-5 * np.sqrt(res["desc"]["K"]) if kind == "f32" else 1e-2
-    worst = float(np.max(np.abs(got - ref) / (tol * np.maximum(np.abs(ref), rms))))
-    return {"rows": int(len(sel)), "max_err_over_tol": round(worst, 4), "pass": worst <= 1.0}
+def extra_line(kind: str, steps: int, warmup: int) -> dict:
+    """Timing plus an oracle parity check for one more configuration: the
+    whole output for C1 and C4, 64 sampled rows otherwise."""
+    from oracle import oracle as O
+    steps = max(10, steps // 2) if kind not in ("c1",) else max(50, steps)
+    r = time_gpu(kind, steps, warmup)
+    r["steps"] = steps
+    d = r["desc"]
+    v = r["flops"] * steps / (r["total_ms"] * 1e-3) / 1e12
+    rows_total = d["batch"] * d["M"]
+    if kind in ("c1", "c4"):
+        sel = np.arange(rows_total, dtype=np.int64)
+    else:
+        sel = np.sort(np.random.default_rng(11).choice(rows_total, size=64, replace=False)).astype(np.int64)
+    av, bv = _views(r["host"])
+    ref = O.matmul(av, bv, rows=sel, nthreads=min(os.cpu_count() or 1, 16))
+    peak = PEAK["bf16" if kind == "bf16" else "f32"]
+    line = {"config": d, "value": round(v, 2), "unit": "TFLOP/s", "pct_of_peak": round(100 * v / peak, 2),
+            "ms_per_step": round(r["total_ms"] / steps, 4),
+            "median_launch_ms": round(r["per_ms"][len(r["per_ms"]) // 2], 4),
+            "parity_spot_check": spot_check(kind, r, (sel, ref), r["host"])}
+    if kind == "c1":
+        line["us_per_launch"] = round(1e3 * r["total_ms"] / steps, 2)
+        line["note"] = "launch-latency bound (0.2 us of MFMA work at peak); no roofline target"
+    if kind in ("bf16", "f32"):
+        line["roofline"] = roofline(kind, r)
+    return line
 
 
 def main():
@@ -214,8 +350,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=["f32", "bf16", "mlp"], default="f32",
-                    help="f32 / bf16 time one GEMM; mlp times the MLP step alone (for profiling)")
+    ap.add_argument("--workload", choices=["f32", "bf16", "mlp", "c1", "c2odd", "c4"], default="f32",
+                    help="f32 / bf16 (the headline configurations) or c1 / c2odd / c4 time one GEMM; mlp times "
+                         "the MLP step alone (for profiling)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the extra workload")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB device copy (10x), the reference for rocprofv3 "
@@ -254,29 +391,23 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if main_kind == "f32" else "bf16",
+        "dtype": "bf16" if main_kind == "bf16" else "f32",
         "data": "synthetic",
         "config": res["desc"],
-        "pct_of_peak": round(100 * value / PEAK[main_kind], 2),
+        "pct_of_peak": round(100 * value / PEAK["bf16" if main_kind == "bf16" else "f32"], 2),
         "median_launch_ms": round(res["per_ms"][len(res["per_ms"]) // 2], 4),
         "roofline": roofline(main_kind, res),
     }
     if not args.no_cpu:
         cb, sample = cpu_baseline(main_kind, res["host"], res["desc"])
         line["cpu_baseline"] = cb
-        line["parity_spot_check"] = spot_check(main_kind, res, sample)
-        other = "bf16" if main_kind == "f32" else "f32"
+        line["parity_spot_check"] = spot_check(main_kind, res, sample, res["host"])
         del res
-        r2 = time_gpu(other, max(10, args.steps // 2), args.warmup)
-        r2["steps"] = max(10, args.steps // 2)
-        v2 = r2["flops"] * r2["steps"] / (r2["total_ms"] * 1e-3) / 1e12
-        line["extra"] = {other: {"config": r2["desc"], "value": round(v2, 2), "unit": "TFLOP/s",
-                                 "pct_of_peak": round(100 * v2 / PEAK[other], 2),
-                                 "ms_per_step": round(r2["total_ms"] / r2["steps"], 4),
-                                 "median_launch_ms": round(r2["per_ms"][len(r2["per_ms"]) // 2], 4),
-                                 "roofline": roofline(other, r2)}}
-        del r2
-        line["extra"]["mlp"] = time_mlp(max(3, args.steps // 10), 1)
+        line["extra"] = {}
+        others = [k for k in ("bf16", "f32") if k != main_kind] + ["c1", "c2odd", "c4"]
+        for other in others:
+            line["extra"][other] = extra_line(other, args.steps, args.warmup)
+        line["extra"]["mlp"] = time_mlp(max(3, args.steps // 10), 2)
     print(json.dumps(line), flush=True)
 
 

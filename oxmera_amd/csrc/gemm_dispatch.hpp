@@ -49,4 +49,29 @@ hipError_t pick_a(const GemmArgs &a, int la, int lb, hipStream_t s) {
     }
 }
 
+// f32 with at least one ragged operand: both vector operands take the
+// ragged loaders (they are correct for whole rows too).
+template <int BM, int BN, int WM, int WN, Ld LA>
+hipError_t pick_b_ragged(const GemmArgs &a, int lb, hipStream_t s) {
+    switch (lb) {
+    case kLdK:
+    case kLdKR: return launch_one<float, BM, BN, WM, WN, LA, Ld::KR>(a, s);
+    case kLdMN:
+    case kLdMNR: return launch_one<float, BM, BN, WM, WN, LA, Ld::MNR>(a, s);
+    default: return launch_one<float, BM, BN, WM, WN, LA, Ld::G>(a, s);
+    }
+}
+
+template <int BM, int BN, int WM, int WN>
+hipError_t pick_a_f32(const GemmArgs &a, int la, int lb, hipStream_t s) {
+    if (la != kLdKR && la != kLdMNR && lb != kLdKR && lb != kLdMNR) return pick_a<float, BM, BN, WM, WN>(a, la, lb, s);
+    switch (la) {
+    case kLdK:
+    case kLdKR: return pick_b_ragged<BM, BN, WM, WN, Ld::KR>(a, lb, s);
+    case kLdMN:
+    case kLdMNR: return pick_b_ragged<BM, BN, WM, WN, Ld::MNR>(a, lb, s);
+    default: return pick_b_ragged<BM, BN, WM, WN, Ld::G>(a, lb, s);
+    }
+}
+
 }  // namespace oxm

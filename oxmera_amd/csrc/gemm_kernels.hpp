@@ -17,8 +17,11 @@
 //      Ld::K   K-contiguous rows, 16-byte loads along K;
 //      Ld::MN  M/N-contiguous columns, 16-byte loads along M/N and a
 //              register transpose before the LDS store;
-//      Ld::G   anything else (odd leading dims, non-unit strides, negative
-//              strides): element loads with per-element bounds.
+//      Ld::KR, Ld::MNR  the same for f32 rows whose length (K, or M/N) is
+//              not a multiple of 4: the straddling chunk is loaded as the
+//              row's last 16 bytes and shifted into place;
+//      Ld::G   anything else (non-unit or negative strides, 16-bit rows
+//              not 16-byte aligned): element loads with per-element bounds.
 //  * Two LDS buffers: the global loads for step k+1 are issued before the
 //    MFMAs of step k and stored to the other buffer after them; one
 //    workgroup barrier per step.
@@ -51,7 +54,7 @@ struct f16_t {
     uint16_t bits;
 };
 
-enum class Ld : int { K = 0, MN = 1, G = 2 };
+enum class Ld : int { K = 0, MN = 1, G = 2, KR = 3, MNR = 4 };
 
 template <typename T>
 struct Elem;
@@ -131,7 +134,7 @@ typedef int i32x4_t __attribute__((ext_vector_type(4)));
 // Byte offsets at or beyond a resource's num_records read as zero; kOob is
 // never inside a resource (num_records <= kMaxRec).
 constexpr uint32_t kMaxRec = 0x7FFFFF00u;
-constexpr uint32_t kOob = 0x7FFFFFF0u;
+constexpr uint32_t kOob = 0x7FFFFFE0u;  // + up to 16 bytes stays below 2^31
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const char *base, int64_t nbytes) {
     if (nbytes < 0) nbytes = 0;
@@ -144,20 +147,41 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// A 16-byte chunk moved down by `bytes` (0 < bytes < 16) with zeros shifted
+// in at the top: element e of the result is element e + bytes/size of `v`.
+// Used for the chunk that straddles the end of a row whose length is not a
+// multiple of the vector width: the last 16 bytes of the row are loaded
+// (always inside it) and shifted so the chunk's valid elements come first.
+__device__ __forceinline__ uint4 shift_down_bytes(uint4 v, int bytes) {
+    // branch-free in `bytes` (0 <= bytes < 16; 0 returns v)
+    const uint64_t lo = (uint64_t)v.x | ((uint64_t)v.y << 32), hi = (uint64_t)v.z | ((uint64_t)v.w << 32);
+    const int b = 8 * bytes;
+    const uint64_t lo_small = (lo >> (b & 63)) | (b ? hi << ((64 - b) & 63) : 0);
+    const uint64_t lo_big = hi >> ((b - 64) & 63);
+    const uint64_t nlo = b >= 64 ? lo_big : lo_small;
+    const uint64_t nhi = b >= 64 ? 0 : hi >> (b & 63);
+    return make_uint4((uint32_t)nlo, (uint32_t)(nlo >> 32), (uint32_t)nhi, (uint32_t)(nhi >> 32));
+}
+
 // ---- global -> LDS loaders -----------------------------------------------
 
 // Loads one operand tile (ROWS rows of the M or N dimension, BK = 128 B of K
 // per row) per K step.  `base` points at (batch, first row of the tile,
 // k = 0); `s_mn`/`s_k` are element strides; `rows_left` = rows of the tile
 // that exist (MN - tile origin); K is the full reduction length.  The host
-// only selects Ld::K / Ld::MN when the strides are non-negative, aligned to
-// 16 bytes and the tile's byte range fits a buffer resource.
+// only selects Ld::K / Ld::MN when the strides are non-negative and the
+// tile's byte range fits a buffer resource; 16-bit operands must also be
+// 16-byte aligned with K (Ld::K) or M/N (Ld::MN) a multiple of 8, while f32
+// rows may start at any 4-byte boundary (16-byte loads need only dword
+// alignment) and end mid-chunk, provided a row (Ld::K: K; Ld::MN: every
+// tile's M/N extent) holds at least one whole chunk.
 template <typename T, Ld KIND, int ROWS, int NT, int NSET>
 struct Loader;
 
 // K-contiguous rows: thread t owns chunk (t % 8) of rows t/8, t/8 + NT/8, ...
-template <typename T, int ROWS, int NT, int NSET>
-struct Loader<T, Ld::K, ROWS, NT, NSET> {
+// RG: K need not be a multiple of kVec (Ld::KR).
+template <typename T, int ROWS, int NT, int NSET, bool RG>
+struct LoaderK {
     static constexpr int kBytes = Elem<T>::kBytes;
     static constexpr int kVec = 16 / kBytes;
     static constexpr int kBK = 128 / kBytes;
@@ -171,8 +195,8 @@ struct Loader<T, Ld::K, ROWS, NT, NSET> {
     int64_t K;
     uint4 regs[NSET][kPer];  // staging sets (NSET = prefetch distance)
 
-    __device__ __forceinline__ Loader(const char *b, int64_t s_mn, int64_t /*s_k*/, int64_t rows_left, int64_t k,
-                                      int tid)
+    __device__ __forceinline__ LoaderK(const char *b, int64_t s_mn, int64_t /*s_k*/, int64_t rows_left, int64_t k,
+                                       int tid)
         : base(b), K(k) {
         chunk = tid & 7;
         const int64_t rows_here = rows_left < ROWS ? rows_left : ROWS;
@@ -183,16 +207,43 @@ struct Loader<T, Ld::K, ROWS, NT, NSET> {
             off[i] = r < rows_left ? (uint32_t)(r * s_mn * kBytes + chunk * 16) : kOob;
         }
     }
+    // Bytes the chunk of step kt must be shifted down by: non-zero only for
+    // the chunk that straddles K (K not a multiple of kVec, K >= kVec), which
+    // is loaded as the row's last kVec elements.
+    __device__ __forceinline__ int tail_shift(int kt) const {
+        const int64_t kc = (int64_t)kt * kBK + chunk * kVec;
+        return (kc < K && kc + kVec > K) ? (int)(kc + kVec - K) * kBytes : 0;
+    }
     template <int S>
     __device__ __forceinline__ void prefetch(int kt) {
         const int64_t k0 = (int64_t)kt * kBK;
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + k0 * kBytes, nbytes - k0 * kBytes);
-        const bool k_ok = (k0 + kBK <= K) || (k0 + chunk * kVec < K);
+        if constexpr (!RG) {
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + k0 * kBytes, nbytes - k0 * kBytes);
+            const bool k_ok = (k0 + kBK <= K) || (k0 + chunk * kVec < K);
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) regs[S][i] = buf_load16(rs, k_ok ? off[i] : kOob);
+            for (int i = 0; i < kPer; ++i) regs[S][i] = buf_load16(rs, k_ok ? off[i] : kOob);
+        } else if (k0 + kBK <= K) {
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + k0 * kBytes, nbytes - k0 * kBytes);
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) regs[S][i] = buf_load16(rs, off[i]);
+        } else {
+            // last step: the resource starts kVec elements early so a shifted
+            // chunk's offset stays non-negative
+            const int64_t back = k0 >= kVec ? kVec : 0;
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(base + (k0 - back) * kBytes, nbytes - (k0 - back) * kBytes);
+            const bool in = k0 + chunk * kVec < K;
+            const uint32_t adj = (uint32_t)(back * kBytes - tail_shift(kt));
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) regs[S][i] = buf_load16(rs, in ? off[i] + adj : kOob);
+        }
     }
     template <int S>
-    __device__ __forceinline__ void store(uint8_t *lds, int tid, int /*kt*/) {
+    __device__ __forceinline__ void store(uint8_t *lds, int tid, int kt) {
+        if (RG && (int64_t)kt * kBK + kBK > K && (K & (kVec - 1)) != 0) {  // uniform: ragged last step
+            const int sh = tail_shift(kt);
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) regs[S][i] = shift_down_bytes(regs[S][i], sh);
+        }
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             int r = (tid >> 3) + i * (NT / 8);
@@ -201,12 +252,22 @@ struct Loader<T, Ld::K, ROWS, NT, NSET> {
     }
 };
 
+template <typename T, int ROWS, int NT, int NSET>
+struct Loader<T, Ld::K, ROWS, NT, NSET> : LoaderK<T, ROWS, NT, NSET, false> {
+    using LoaderK<T, ROWS, NT, NSET, false>::LoaderK;
+};
+template <typename T, int ROWS, int NT, int NSET>
+struct Loader<T, Ld::KR, ROWS, NT, NSET> : LoaderK<T, ROWS, NT, NSET, true> {
+    using LoaderK<T, ROWS, NT, NSET, true>::LoaderK;
+};
+
 // M/N-contiguous columns: thread t owns a kVec(mn) x kVec(k) block, k-block
 // t % 8; kVec 16-byte loads along MN are transposed in registers into kVec
 // K-major 16-byte chunks.  Blocks are assigned so that the two 8-lane halves
 // of every 16-lane LDS phase write rows 8 apart (opposite bank halves).
-template <typename T, int ROWS, int NT, int NSET>
-struct Loader<T, Ld::MN, ROWS, NT, NSET> {
+// RG: M/N need not be a multiple of kVec (Ld::MNR).
+template <typename T, int ROWS, int NT, int NSET, bool RG>
+struct LoaderMN {
     static constexpr int kBytes = Elem<T>::kBytes;
     static constexpr int kVec = 16 / kBytes;
     static constexpr int kBK = 128 / kBytes;
@@ -218,7 +279,9 @@ struct Loader<T, Ld::MN, ROWS, NT, NSET> {
     int64_t nbytes, sk_bytes;
     uint32_t off[kPer];
     int mb[kPer];
+    int shift[kPer];  // bytes a block straddling a ragged M/N edge is shifted down by
     bool ok[kPer];
+    bool ragged;      // tile-uniform: some block straddles the M/N edge
     bool active;
     int kb;
     int64_t K;
@@ -234,19 +297,24 @@ struct Loader<T, Ld::MN, ROWS, NT, NSET> {
         }
     }
 
-    __device__ __forceinline__ Loader(const char *b, int64_t /*s_mn*/, int64_t s_k, int64_t rows_left, int64_t k,
-                                      int tid)
+    __device__ __forceinline__ LoaderMN(const char *b, int64_t /*s_mn*/, int64_t s_k, int64_t rows_left, int64_t k,
+                                        int tid)
         : base(b), K(k) {
         sk_bytes = s_k * kBytes;
         kb = tid & 7;
         active = tid < kBlocks * kPer;
         const int64_t rows_here = rows_left < ROWS ? rows_left : ROWS;
+        ragged = RG && (rows_here & (kVec - 1)) != 0;
         nbytes = (k - 1) * sk_bytes + rows_here * kBytes;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             mb[i] = block_of((tid >> 3) + i * (NT / 8));
             ok[i] = active && (int64_t)mb[i] * kVec < rows_left;
-            off[i] = (uint32_t)(mb[i] * 16 + kb * kVec * sk_bytes);
+            // A block that straddles the edge (the tile holds >= kVec rows, so
+            // it is not the first) loads the last kVec rows and is shifted.
+            const int nv = (int)rows_here - mb[i] * kVec;
+            shift[i] = (RG && ok[i] && nv < kVec) ? (kVec - nv) * kBytes : 0;
+            off[i] = (uint32_t)(mb[i] * 16 - shift[i] + kb * kVec * sk_bytes);
         }
     }
     template <int S>
@@ -266,6 +334,12 @@ struct Loader<T, Ld::MN, ROWS, NT, NSET> {
     template <int S>
     __device__ __forceinline__ void store(uint8_t *lds, int /*tid*/, int /*kt*/) {
         if (!active) return;
+        if (RG && ragged) {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i)
+#pragma unroll
+                for (int j = 0; j < kVec; ++j) regs[S][i][j] = shift_down_bytes(regs[S][i][j], shift[i]);
+        }
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             if constexpr (kBytes == 4) {
@@ -295,6 +369,15 @@ struct Loader<T, Ld::MN, ROWS, NT, NSET> {
             }
         }
     }
+};
+
+template <typename T, int ROWS, int NT, int NSET>
+struct Loader<T, Ld::MN, ROWS, NT, NSET> : LoaderMN<T, ROWS, NT, NSET, false> {
+    using LoaderMN<T, ROWS, NT, NSET, false>::LoaderMN;
+};
+template <typename T, int ROWS, int NT, int NSET>
+struct Loader<T, Ld::MNR, ROWS, NT, NSET> : LoaderMN<T, ROWS, NT, NSET, true> {
+    using LoaderMN<T, ROWS, NT, NSET, true>::LoaderMN;
 };
 
 // Generic strided operand: element loads with full bounds checks, issued in

@@ -7,7 +7,9 @@
 namespace oxm {
 
 // Operand loader kinds (the kernel's Ld enum, as plain ints for the host).
-enum LoaderKind : int { kLdK = 0, kLdMN = 1, kLdG = 2 };
+// kLdKR / kLdMNR: f32 K- / M/N-contiguous rows whose length is not a
+// multiple of 4 (the kernels shift the straddling chunk into place).
+enum LoaderKind : int { kLdK = 0, kLdMN = 1, kLdG = 2, kLdKR = 3, kLdMNR = 4 };
 
 // Tile configurations.
 enum TileCfg : int {

@@ -223,11 +223,27 @@ int classify(const char *ptr, int64_t s_mn, int64_t s_k, int64_t mn, int64_t k, 
              int es, int tile_rows) {
     const int64_t vec = 16 / es;
     const int64_t kMaxRec = 0x7FFFFF00LL;
+    if (mn == 1) s_mn = 0;
+    if (k == 1) s_k = 0;
+    if (es == 4) {
+        // f32: 16-byte loads need only dword alignment and the loaders
+        // handle rows that end mid-chunk, so any non-negative unit-stride
+        // layout qualifies.
+        // A ragged row needs one whole chunk inside it: K >= 4 (Ld::K), and
+        // for Ld::MN at least 4 elements in the last, partial tile.
+        const bool al4 = ((uintptr_t)ptr % 4) == 0;
+        const int64_t edge = mn % tile_rows;
+        if (al4 && s_k == 1 && s_mn >= 0 && (k % vec == 0 || k >= vec) &&
+            ((int64_t)tile_rows * s_mn + k) * es <= kMaxRec)
+            return k % vec == 0 ? oxm::kLdK : oxm::kLdKR;
+        if (al4 && s_mn == 1 && s_k >= 0 && (mn % vec == 0 || edge == 0 || edge >= vec) &&
+            (k * s_k + tile_rows) * es <= kMaxRec)
+            return mn % vec == 0 ? oxm::kLdMN : oxm::kLdMNR;
+        return oxm::kLdG;
+    }
     bool aligned = ((uintptr_t)ptr % 16) == 0;
     bool batch_ok = true;
     for (int d = 0; d < nbd; ++d) batch_ok = batch_ok && (bstr[d] % vec == 0);
-    if (mn == 1) s_mn = 0;
-    if (k == 1) s_k = 0;
     if (aligned && batch_ok && s_k == 1 && k % vec == 0 && s_mn % vec == 0 && s_mn >= 0 &&
         ((int64_t)tile_rows * s_mn + k) * es <= kMaxRec)
         return oxm::kLdK;
@@ -235,6 +251,22 @@ int classify(const char *ptr, int64_t s_mn, int64_t s_k, int64_t mn, int64_t k, 
         (k * s_k + tile_rows) * es <= kMaxRec)
         return oxm::kLdMN;
     return oxm::kLdG;
+}
+
+// Tile size from a wave-count model of the 256-CU chip.  A 256x256 tile
+// occupies a whole CU (128 KB of LDS), so n256 tiles take ceil(n256 / 256)
+// rounds; 128x128 tiles run two per CU, a round of 512 of them taking 0.57
+// of a 256x256 round (measured at 4096^3 f32 and 8192^3 bf16), and a part
+// round costs its share.  E.g. 4096^3: 1 round vs 1.14 -> 256x256;
+// 4097x4095 (272 big tiles): 2 rounds vs 1.18 -> 128x128; C4's 32 batches
+// of 512x768: 1 round vs 0.86 -> 128x128.
+bool prefer_256_tiles(int64_t M, int64_t N, int64_t batch) {
+    const int64_t n256 = ((M + 255) / 256) * ((N + 255) / 256) * batch;
+    const int64_t n128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
+    const double rounds256 = (double)((n256 + 255) / 256);
+    double rounds128 = (double)n128 / 512.0;
+    if (rounds128 < 0.5) rounds128 = 0.5;
+    return rounds256 < 0.57 * rounds128;
 }
 
 int env_int(const char *name, int dflt) {
@@ -394,14 +426,13 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     g.bias_dtype = ep->bias_dtype;
 
     int cfg;
-    const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
+    const bool big = prefer_256_tiles(M, N, batch);
     if (a->dtype == OXM_F32) {
-        // 256x256 tiles once they fill the 256 CUs, 128x128 below that
-        cfg = big_tiles >= 256 ? oxm::kCfgF32_256 : oxm::kCfgF32_128;
+        cfg = big ? oxm::kCfgF32_256 : oxm::kCfgF32_128;
         cfg = env_int("OXM_GEMM_CFG_F32", cfg);
         if (cfg != oxm::kCfgF32_256) cfg = oxm::kCfgF32_128;
     } else {
-        cfg = big_tiles >= 256 ? oxm::kCfgH_256 : oxm::kCfgH_128;
+        cfg = big ? oxm::kCfgH_256 : oxm::kCfgH_128;
         cfg = env_int("OXM_GEMM_CFG", cfg);
         if (cfg < oxm::kCfgH_256 || cfg > oxm::kCfgH_256_NS) cfg = oxm::kCfgH_128;
     }

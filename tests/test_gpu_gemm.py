@@ -113,6 +113,39 @@ def test_layouts_full(hip, dtype, la, lb):
         assert_close(to_f32(c), ref, spec_tolerance(dtype, k), f"{dtype.name} {la}x{lb} {m}x{k}x{n}")
 
 
+RAGGED = [(5, 3, 7), (129, 13, 131), (300, 257, 259), (257, 1, 6), (70, 130, 65), (33, 66, 1)]
+
+
+@pytest.mark.parametrize("a_major", ["k", "m"])
+@pytest.mark.parametrize("b_major", ["k", "n"])
+def test_f32_ragged_unit_stride_rows(hip, a_major, b_major):
+    """f32 operands with unit stride along K (or M/N) whose rows start at any
+    4-byte boundary and whose length is not a multiple of 4: they take the
+    vector loaders, with the last chunk of each row loaded element by element."""
+    for si, (m, k, n) in enumerate(RAGGED):
+        rng = np.random.default_rng(77 + si)
+        off_a, off_b = 1 + si % 3, 3 - si % 3
+        if a_major == "k":   # [m, k] rows of length k, leading dim k + 1
+            lda = k + 1
+            abuf = host_buffer(F32, rng.uniform(-1, 1, off_a + m * lda).astype(np.float32))
+            a = Operand(F32, abuf, (m, k), (lda, 1), off_a)
+        else:                # M-contiguous, leading dim m + 3
+            lda = m + 3
+            abuf = host_buffer(F32, rng.uniform(-1, 1, off_a + k * lda).astype(np.float32))
+            a = Operand(F32, abuf, (m, k), (1, lda), off_a)
+        if b_major == "n":   # [k, n] rows of length n, leading dim n + 2
+            ldb = n + 2
+            bbuf = host_buffer(F32, rng.uniform(-1, 1, off_b + k * ldb).astype(np.float32))
+            b = Operand(F32, bbuf, (k, n), (ldb, 1), off_b)
+        else:                # K-contiguous, leading dim k + 5
+            ldb = k + 5
+            bbuf = host_buffer(F32, rng.uniform(-1, 1, off_b + n * ldb).astype(np.float32))
+            b = Operand(F32, bbuf, (k, n), (1, ldb), off_b)
+        log(f"ragged f32 A {a_major}-major B {b_major}-major M={m} K={k} N={n}")
+        c = hip.matmul(a.dev, b.dev)
+        assert_close(to_f32(c), O.matmul(a.ora, b.ora), spec_tolerance(F32, k), f"ragged {m}x{k}x{n}")
+
+
 @pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
 def test_batched_broadcast_small(hip, dtype):
     rng = np.random.default_rng(3)
