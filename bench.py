@@ -176,10 +176,10 @@ def time_mlp(steps: int, warmup: int):
     be.set_stream(stream.cuda_stream)
     try:
         with torch.cuda.stream(stream):
-            t0, n = time.perf_counter(), 0
-            while n < warmup or time.perf_counter() - t0 < WARMUP_S:
+            w0, nw = time.perf_counter(), 0
+            while nw < warmup or time.perf_counter() - w0 < WARMUP_S:
                 model.train_step(x, t)
-                n += 1
+                nw += 1
                 torch.cuda.synchronize()
             start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record(stream)

@@ -89,12 +89,18 @@ typedef struct {
 /* Fused epilogue.  bias: [N] of bias_dtype on the device, or NULL.  aux: a
  * contiguous [batch..., M, N] buffer of out_dtype: written with the
  * pre-activation for OXM_ACT_GELU (may be NULL), read as Z for OXM_ACT_DGELU
- * (required).  out_dtype must equal the dtype of the output view. */
+ * (required).  out_dtype must equal the dtype of the output view.
+ * colsum: an F32 [N] device buffer, or NULL; when set, the call overwrites it
+ * with the sums over all rows (and batches) of the output AS STORED (after
+ * rounding to the output dtype) -- the bias gradient of a Linear layer whose
+ * input gradient this GEMM produces (ReduceOps::sum over rows,
+ * crates/oxmera-ops/src/lib.rs:61-69, fused into the producer). */
 typedef struct {
     const void *bias;
     int32_t bias_dtype;
     int32_t act;             /* oxm_act */
     void *aux;
+    float *colsum;
 } oxm_epilogue;
 
 /* Library version string. */
@@ -144,9 +150,12 @@ oxm_status oxm_sum_rows(const oxm_view *x, const oxm_view *out, void *stream);
 /* Mean-squared-error loss and its gradient (the MLP's objective; composed in
  * the reference from BinaryOps::sub/mul and ReduceOps::sum,
  * crates/oxmera-ops/src/lib.rs:39-69): loss[0] = mean((y - t)^2) (f32, device),
- * dy = 2 (y - t) / numel in dy's dtype.  y, t, dy: contiguous, same shape. */
+ * dy = 2 (y - t) / numel in dy's dtype.  y, t, dy: contiguous, same shape.
+ * dy_colsum: NULL, or an F32 [C] view (C = the last dimension) that receives
+ * the sums over the leading dimensions of dy as stored -- the bias gradient of
+ * the layer that produced y, in the same pass. */
 oxm_status oxm_mse_loss_grad(const oxm_view *y, const oxm_view *t, const oxm_view *loss, const oxm_view *dy,
-                             void *stream);
+                             const oxm_view *dy_colsum, void *stream);
 
 /* Storage for device tensors (crates/oxmera-tensor/src/storage.rs:12-32,
  * "GPU variants hold opaque backend handles", :19-24). */

@@ -52,6 +52,7 @@ class OxmEpilogue(C.Structure):
         ("bias_dtype", C.c_int32),
         ("act", C.c_int32),
         ("aux", C.c_void_p),
+        ("colsum", C.c_void_p),
     ]
 
 
@@ -69,7 +70,7 @@ _PROTOS = {
                            C.POINTER(OxmEpilogue), C.c_void_p]),
     "oxm_sum_rows": (C.c_int, [C.POINTER(OxmView), C.POINTER(OxmView), C.c_void_p]),
     "oxm_mse_loss_grad": (C.c_int, [C.POINTER(OxmView), C.POINTER(OxmView), C.POINTER(OxmView),
-                                    C.POINTER(OxmView), C.c_void_p]),
+                                    C.POINTER(OxmView), C.POINTER(OxmView), C.c_void_p]),
     "oxm_alloc": (C.c_int, [C.c_int32, C.c_size_t, C.POINTER(C.c_void_p)]),
     "oxm_free": (C.c_int, [C.c_int32, C.c_void_p]),
     "oxm_copy": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_size_t, C.c_void_p]),

@@ -10,7 +10,9 @@ exactly the GEMMs of that model on the HIP backend:
   backward  dW = x^T . dz          A is a transposed VIEW of x (no copy)
             dx = dz . W^T          B is a transposed VIEW of W; when x came out of
                                    a GELU layer, GELU'(z) is fused into this GEMM
-            db = sum over rows of dz
+            db = sum over rows of dz, formed by whichever kernel produces dz:
+                                   the MSE pass (dy) or the dx GEMM's epilogue
+                                   (GELU' fused), from the values as stored
 
 Weight and bias gradients are f32; activation gradients keep the
 activation dtype.
@@ -46,6 +48,10 @@ class _LinearNode:
     def __init__(self, x: Var, w: Var, b: Optional[Var], act: int, z: Optional[Tensor]):
         self.x, self.w, self.b, self.act, self.z = x, w, b, act, z
         self.out: Optional[Var] = None
+        self.db: Optional[Tensor] = None  # bias gradient formed by the producer of dz
+
+    def wants_db(self) -> bool:
+        return self.b is not None and self.b.requires_grad
 
     def parents(self):
         return [v for v in (self.x, self.w, self.b) if v is not None]
@@ -60,14 +66,22 @@ class _LinearNode:
         if self.w.requires_grad:
             # dW = x^T . dz  (x^T is a stride view)
             _set_grad(self.w, be.matmul(x2.transpose_last(), dz2, out_dtype=DType.F32), False)
-        if self.b is not None and self.b.requires_grad:
-            _set_grad(self.b, be.sum(dz2, [0]), False)
+        if self.wants_db():
+            _set_grad(self.b, self.db if self.db is not None else be.sum(dz2, [0]), False)
         if self.x.requires_grad:
             prod = self.x.node
             fuse = isinstance(prod, _LinearNode) and prod.act == _lib.ACT_GELU
-            # dx = dz . W^T  (W^T is a stride view), GELU'(z_prev) fused when x = GELU(z_prev)
+            # dx = dz . W^T  (W^T is a stride view), GELU'(z_prev) fused when x = GELU(z_prev);
+            # then dx is the producer layer's dz, and its bias gradient comes out of
+            # the same epilogue
+            db_prev = None
+            if fuse and prod.wants_db():
+                db_prev = Tensor.empty((self.w.t.shape[0],), DType.F32, dz.device)
             dx = be.matmul(dz, self.w.t.transpose_last(), out_dtype=self.x.t.dtype,
-                           act=_lib.ACT_DGELU if fuse else _lib.ACT_NONE, aux=prod.z if fuse else None)
+                           act=_lib.ACT_DGELU if fuse else _lib.ACT_NONE, aux=prod.z if fuse else None,
+                           colsum=db_prev)
+            if db_prev is not None:
+                prod.db = db_prev
             _set_grad(self.x, dx, fuse)
 
 
@@ -109,7 +123,13 @@ def mse_loss(y: Var, target: Tensor) -> Var:
     """mean((y - t)^2) as a one-element F32 tensor; the gradient is formed in
     the same pass."""
     be = backend_for(y.t.device)
-    loss, dy = be.mse_loss_grad(y.t, target)
+    prod = y.node
+    db = None
+    if y.requires_grad and isinstance(prod, _LinearNode) and prod.act == _lib.ACT_NONE and prod.wants_db():
+        db = Tensor.empty((y.t.shape[-1],), DType.F32, y.t.device)  # its bias gradient, in the same pass
+    loss, dy = be.mse_loss_grad(y.t, target, dy_colsum=db)
+    if db is not None:
+        prod.db = db
     node = _MSENode(y, dy) if y.requires_grad else None
     return Var(loss, y.requires_grad, node)
 

@@ -52,10 +52,11 @@ class HipBackend:
     # ---- MatmulOps ----
     def matmul(self, lhs: Tensor, rhs: Tensor, *, out_dtype: DType | None = None, bias: Tensor | None = None,
                act: int = _lib.ACT_NONE, aux: Tensor | None = None, out: Tensor | None = None,
-               stream: int | None = None) -> Tensor:
+               colsum: Tensor | None = None, stream: int | None = None) -> Tensor:
         """``lhs . rhs`` into a fresh contiguous tensor (or ``out``), with an
         optional fused epilogue (bias, GELU / GELU-backward).  Operands are any
-        strided views; nothing is copied."""
+        strided views; nothing is copied.  ``colsum`` (F32 [N]) receives the
+        sums over rows of the output as stored (a bias gradient)."""
         a, b = lhs.abi_view(), rhs.abi_view()
         nd = C.c_int32(0)
         shp = (C.c_int64 * _lib.MAX_DIMS)()
@@ -66,10 +67,13 @@ class HipBackend:
             out = Tensor.empty(oshape, odt, lhs.device)
         c = out.abi_view()
         ep = None
-        if bias is not None or act != _lib.ACT_NONE or aux is not None:
+        if bias is not None or act != _lib.ACT_NONE or aux is not None or colsum is not None:
+            if colsum is not None and (colsum.dtype != DType.F32 or colsum.shape != (oshape[-1],)):
+                raise ValueError(f"colsum must be F32 [{oshape[-1]}], got {colsum.dtype.name} {list(colsum.shape)}")
             ep = _lib.OxmEpilogue(C.c_void_p(bias.data_ptr() if bias is not None else 0),
                                   int(bias.dtype) if bias is not None else 0, int(act),
-                                  C.c_void_p(aux.data_ptr() if aux is not None else 0))
+                                  C.c_void_p(aux.data_ptr() if aux is not None else 0),
+                                  C.c_void_p(colsum.data_ptr() if colsum is not None else 0))
         check(_lib.lib().oxm_gemm(C.byref(a), C.byref(b), C.byref(c), C.byref(ep) if ep is not None else None,
                                   self._s(stream)))
         return out
@@ -108,12 +112,16 @@ class HipBackend:
     def div(self, lhs, rhs): self._absent("div")
 
     # ---- loss (MSE and its gradient in one pass) ----
-    def mse_loss_grad(self, y: Tensor, t: Tensor, *, stream: int | None = None) -> tuple[Tensor, Tensor]:
+    def mse_loss_grad(self, y: Tensor, t: Tensor, *, dy_colsum: Tensor | None = None,
+                      stream: int | None = None) -> tuple[Tensor, Tensor]:
+        """(loss, dy); ``dy_colsum`` (F32 [C]) also receives the sums of dy over
+        its leading dimensions, in the same pass."""
         loss = Tensor.empty((1,), DType.F32, y.device)
         dy = Tensor.empty(y.shape, y.dtype, y.device)
         vy, vt, vl, vd = y.abi_view(), t.abi_view(), loss.abi_view(), dy.abi_view()
+        vc = dy_colsum.abi_view() if dy_colsum is not None else None
         check(_lib.lib().oxm_mse_loss_grad(C.byref(vy), C.byref(vt), C.byref(vl), C.byref(vd),
-                                           self._s(stream)))
+                                           C.byref(vc) if vc is not None else None, self._s(stream)))
         return loss, dy
 
 

@@ -30,6 +30,7 @@ struct GemmArgs {
     int32_t tiles_m, tiles_n;     // tiles per batch
     int32_t group_m;              // tile-row grouping for L2 reuse
     int32_t xcd_remap;            // 1: spread consecutive tiles per XCD
+    float *colsum;                // [N] f32 (zeroed by the host), += column sums of the stored C, or nullptr
 };
 
 }  // namespace oxm

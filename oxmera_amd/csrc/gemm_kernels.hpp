@@ -488,8 +488,23 @@ __device__ __forceinline__ float load_out(const void *c, int64_t i) {
 
 // Stores four consecutive outputs C[o .. o+3] (o = row*N + col), applying the
 // epilogue.  `vec` = the four are in range and 4-element aligned.
+// The value a store of OUT_DT keeps, as f32 (what a later read sees).
 template <int OUT_DT>
-__device__ __forceinline__ void store4(const GemmArgs &p, int64_t o, int64_t col, float4 v, bool vec, int nvalid) {
+__device__ __forceinline__ float stored_value(float x) {
+    if constexpr (OUT_DT == kDtF32)
+        return x;
+    else if constexpr (OUT_DT == kDtBF16)
+        return bf16_bits_to_f32(f32_to_bf16_bits(x));
+    else
+        return f16_bits_to_f32(f32_to_f16_bits(x));
+}
+
+// Applies the epilogue to 4 adjacent outputs (row-major offset o, column col,
+// nvalid of them inside N) and stores them; with p.colsum, adds the stored
+// values to cs.
+template <int OUT_DT>
+__device__ __forceinline__ void store4(const GemmArgs &p, int64_t o, int64_t col, float4 v, bool vec, int nvalid,
+                                       float (&cs)[4]) {
     float x[4] = {v.x, v.y, v.z, v.w};
     if (p.act == kActDGelu) {
 #pragma unroll
@@ -510,6 +525,11 @@ __device__ __forceinline__ void store4(const GemmArgs &p, int64_t o, int64_t col
                 }
             }
         }
+    }
+    if (p.colsum) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i < nvalid) cs[i] += stored_value<OUT_DT>(x[i]);
     }
     if (vec) {
         if constexpr (OUT_DT == kDtF32) {
@@ -533,10 +553,11 @@ __device__ __forceinline__ void store4(const GemmArgs &p, int64_t o, int64_t col
 }
 
 // Writes one 32-row slab of a wave's accumulators (already staged in LDS as
-// f32 [32][WN + 4]) to C with coalesced 4-element stores.
+// f32 [32][WN + 8]) to C with coalesced 4-element stores; lane l owns columns
+// col0 + 4 (l % (WN/4)) .. +3 of rows l / (WN/4), + 64/(WN/4), ...
 template <int OUT_DT, int WN>
 __device__ __forceinline__ void write_slab(const GemmArgs &p, const float *ws, int64_t cbase, int64_t row0,
-                                           int64_t col0, int lane) {
+                                           int64_t col0, int lane, float (&cs)[4]) {
     constexpr int kLanesPerRow = WN / 4;
     constexpr int kRowsPerIter = 64 / kLanesPerRow;
     constexpr int kSld = WN + 8;
@@ -550,8 +571,58 @@ __device__ __forceinline__ void write_slab(const GemmArgs &p, const float *ws, i
         if (row >= p.M || nvalid == 0) continue;
         float4 v = *(const float4 *)(ws + r * kSld + c4);
         int64_t o = cbase + row * p.N + col;
-        store4<OUT_DT>(p, o, col, v, aligned && nvalid == 4, nvalid);
+        store4<OUT_DT>(p, o, col, v, aligned && nvalid == 4, nvalid, cs);
     }
+}
+
+// Adds a wave's column partial sums (cs, per lane as in write_slab) into
+// p.colsum: lanes that own the same columns are summed with cross-lane
+// shuffles, then one lane per column group issues the atomics.
+template <int WN>
+__device__ __forceinline__ void colsum_flush(const GemmArgs &p, float (&cs)[4], int64_t col0, int lane) {
+    constexpr int kLanesPerRow = WN / 4;
+#pragma unroll
+    for (int off = kLanesPerRow; off < 64; off <<= 1)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cs[i] += __shfl_xor(cs[i], off);
+    if (lane < kLanesPerRow) {
+        const int64_t col = col0 + lane * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (col + i < p.N) atomicAdd(p.colsum + col + i, cs[i]);
+    }
+}
+
+// LDS-staged epilogue: each wave writes its WM x WN accumulators one 32-row
+// slab at a time through a padded LDS slab (row stride WN + 8 floats,
+// conflict-free), then stores rows with 16-byte writes, applying the bias and
+// activation.  The caller has drained every DMA into `lds` and synchronised.
+template <int NT, int WM, int WN, int TM, int TN, int LDS_BYTES>
+__device__ __forceinline__ void epilogue_lds(const GemmArgs &p, f32x16_t (&acc)[TM][TN], uint8_t *lds, int wave,
+                                             int lane, int64_t cbase, int64_t row_base, int64_t col0) {
+    const int half = lane >> 5;
+    constexpr int kSld = WN + 8;
+    static_assert(NT / 64 * 32 * kSld * 4 <= LDS_BYTES, "epilogue staging must fit in LDS");
+    float *ws = (float *)lds + wave * 32 * kSld;
+    float cs[4] = {0.f, 0.f, 0.f, 0.f};  // column sums of the stored output (p.colsum)
+    static_for<0, TM>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                ws[(8 * (e >> 2) + 4 * half + (e & 3)) * kSld + j * 32 + (lane & 31)] = acc[i][j][e];
+        __syncthreads();
+        const int64_t row0 = row_base + i * 32;
+        if (p.out_dtype == kDtF32)
+            write_slab<kDtF32, WN>(p, ws, cbase, row0, col0, lane, cs);
+        else if (p.out_dtype == kDtBF16)
+            write_slab<kDtBF16, WN>(p, ws, cbase, row0, col0, lane, cs);
+        else
+            write_slab<kDtF16, WN>(p, ws, cbase, row0, col0, lane, cs);
+        __syncthreads();
+    });
+    if (p.colsum) colsum_flush<WN>(p, cs, col0, lane);
 }
 
 // ---- the kernel -------------------------------------------------------------
@@ -694,32 +765,8 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
         for (int kt = 0; kt < nk; ++kt) k_step(std::integral_constant<int, 0>{}, kt);
     }
 
-    // Epilogue: each wave stages one 32-row slab of its accumulators in LDS
-    // (the operand buffers are free after the last barrier), then stores it
-    // row-contiguously.  32x32 MFMA accumulator layout: lane l, element e is
-    // C[8*(e/4) + 4*(l/32) + e%4][l%32].
-    constexpr int kSld = WN + 8;  // rows 4 apart land on opposite bank halves
-    static_assert(NT / 64 * 32 * kSld * 4 <= 2 * kStage, "epilogue staging must fit in LDS");
-    float *ws = (float *)lds + wave * 32 * kSld;
-    const int64_t cbase = bidx * p.M * p.N;
-    const int64_t col0 = n0 + wn * WN;
-    static_for<0, TM>([&](auto ic) {
-        constexpr int i = decltype(ic)::value;
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-                ws[(8 * (e >> 2) + 4 * half + (e & 3)) * kSld + j * 32 + (lane & 31)] = acc[i][j][e];
-        __syncthreads();
-        const int64_t row0 = m0 + wm * WM + i * 32;
-        if (p.out_dtype == kDtF32)
-            write_slab<kDtF32, WN>(p, ws, cbase, row0, col0, lane);
-        else if (p.out_dtype == kDtBF16)
-            write_slab<kDtBF16, WN>(p, ws, cbase, row0, col0, lane);
-        else
-            write_slab<kDtF16, WN>(p, ws, cbase, row0, col0, lane);
-        __syncthreads();
-    });
+    // Epilogue (the operand buffers are free after the last barrier).
+    epilogue_lds<NT, WM, WN, TM, TN, 2 * kStage>(p, acc, lds, wave, lane, bidx * p.M * p.N, m0 + wm * WM, n0 + wn * WN);
 }
 
 // ===========================================================================
@@ -948,36 +995,6 @@ __device__ __forceinline__ TileCoord tile_coord(const GemmArgs &p, int64_t wg) {
         }
     }
     return tc;
-}
-
-// LDS-staged epilogue: each wave writes its WM x WN accumulators one 32-row
-// slab at a time through a padded LDS slab (row stride WN + 8 floats,
-// conflict-free), then stores rows with 16-byte writes, applying the bias and
-// activation.  The caller has drained every DMA into `lds` and synchronised.
-template <int NT, int WM, int WN, int TM, int TN, int LDS_BYTES>
-__device__ __forceinline__ void epilogue_lds(const GemmArgs &p, f32x16_t (&acc)[TM][TN], uint8_t *lds, int wave,
-                                             int lane, int64_t cbase, int64_t row_base, int64_t col0) {
-    const int half = lane >> 5;
-    constexpr int kSld = WN + 8;
-    static_assert(NT / 64 * 32 * kSld * 4 <= LDS_BYTES, "epilogue staging must fit in LDS");
-    float *ws = (float *)lds + wave * 32 * kSld;
-    static_for<0, TM>([&](auto ic) {
-        constexpr int i = decltype(ic)::value;
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-                ws[(8 * (e >> 2) + 4 * half + (e & 3)) * kSld + j * 32 + (lane & 31)] = acc[i][j][e];
-        __syncthreads();
-        const int64_t row0 = row_base + i * 32;
-        if (p.out_dtype == kDtF32)
-            write_slab<kDtF32, WN>(p, ws, cbase, row0, col0, lane);
-        else if (p.out_dtype == kDtBF16)
-            write_slab<kDtBF16, WN>(p, ws, cbase, row0, col0, lane);
-        else
-            write_slab<kDtF16, WN>(p, ws, cbase, row0, col0, lane);
-        __syncthreads();
-    });
 }
 
 // Direct-to-LDS GEMM for 16-bit operands that are K- or M/N-contiguous

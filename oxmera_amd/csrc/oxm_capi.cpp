@@ -373,7 +373,7 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     if (nbd > oxm::kMaxBatchDims)
         return fail(OXM_E_NOT_IMPLEMENTED, "matmul is not implemented for %d batch dims (max %d)", nbd,
                     oxm::kMaxBatchDims);
-    oxm_epilogue none = {nullptr, OXM_F32, OXM_ACT_NONE, nullptr};
+    oxm_epilogue none = {nullptr, OXM_F32, OXM_ACT_NONE, nullptr, nullptr};
     if (!ep) ep = &none;
     if (ep->act < OXM_ACT_NONE || ep->act > OXM_ACT_DGELU)
         return fail(OXM_E_INVALID_ARGUMENT, "matmul: unknown epilogue activation %d", ep->act);
@@ -385,7 +385,17 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     const int64_t M = oshape[nd - 2], N = oshape[nd - 1], K = a->shape[a->ndim - 1];
     int64_t batch = 1;
     for (int i = 0; i < nbd; ++i) batch *= oshape[i];
-    if (batch == 0 || M == 0 || N == 0) return ok();
+    if (N == 0) return ok();
+    if (batch == 0 || M == 0) {
+        if (!ep->colsum) return ok();
+        // sums over no rows: the column sums are zero
+        DeviceGuard guard(a->device);
+        if ((st = check_device_range(ep->colsum, 0, N * 4, a->device, "colsum", op)) != OXM_OK) return st;
+        hipStream_t s = (hipStream_t)stream;
+        hipError_t e = oxm::launch_fill_zero(ep->colsum, N, s);
+        if (e != hipSuccess) return hip_fail(e, op);
+        return finish(s, op);
+    }
 
     DeviceGuard guard(a->device);
     if ((st = check_view_memory(a, "lhs", op)) != OXM_OK) return st;
@@ -396,6 +406,8 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
                         OXM_OK)
         return st;
     if (ep->aux && (st = check_device_range(ep->aux, 0, batch * M * N * oes, a->device, "aux", op)) != OXM_OK)
+        return st;
+    if (ep->colsum && (st = check_device_range(ep->colsum, 0, N * 4, a->device, "colsum", op)) != OXM_OK)
         return st;
 
     const int es = dtype_size(a->dtype);
@@ -442,6 +454,11 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     int64_t ntiles = ((M + ts.bm - 1) / ts.bm) * ((N + ts.bn - 1) / ts.bn) * batch;
     if (ntiles > 0x7fffffffLL) return fail(OXM_E_NOT_IMPLEMENTED, "matmul is not implemented for %lld tiles", (long long)ntiles);
     hipStream_t s = (hipStream_t)stream;
+    if (ep->colsum) {
+        g.colsum = ep->colsum;
+        hipError_t ez = oxm::launch_fill_zero(ep->colsum, N, s);
+        if (ez != hipSuccess) return hip_fail(ez, op);
+    }
     hipError_t e = oxm::launch_gemm(g, a->dtype, ld_a, ld_b, cfg, s);
     if (e != hipSuccess) return hip_fail(e, op);
     return finish(s, op);
@@ -476,13 +493,14 @@ oxm_status oxm_sum_rows(const oxm_view *x, const oxm_view *out, void *stream) {
 }
 
 oxm_status oxm_mse_loss_grad(const oxm_view *y, const oxm_view *t, const oxm_view *loss, const oxm_view *dy,
-                             void *stream) {
+                             const oxm_view *dy_colsum, void *stream) {
     const char *op = "mse_loss";
     oxm_status st;
     if ((st = check_view(y, "y", op)) != OXM_OK) return st;
     if ((st = check_view(t, "target", op)) != OXM_OK) return st;
     if ((st = check_view(loss, "loss", op)) != OXM_OK) return st;
     if ((st = check_view(dy, "dy", op)) != OXM_OK) return st;
+    if (dy_colsum && (st = check_view(dy_colsum, "dy_colsum", op)) != OXM_OK) return st;
     if (!is_gemm_dtype(y->dtype)) return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by mse_loss", dtype_name(y->dtype));
     if (t->dtype != y->dtype || dy->dtype != y->dtype)
         return fail(OXM_E_DTYPE_MISMATCH, "dtype mismatch: expected %s, got %s in mse_loss", dtype_name(y->dtype),
@@ -499,15 +517,28 @@ oxm_status oxm_mse_loss_grad(const oxm_view *y, const oxm_view *t, const oxm_vie
         return fail(OXM_E_DEVICE_MISMATCH, "device mismatch in mse_loss");
     const int64_t n = numel(y);
     if (n == 0) return fail(OXM_E_SHAPE_MISMATCH, "mse_loss of an empty tensor has no mean");
+    const int64_t C = y->ndim > 0 ? y->shape[y->ndim - 1] : 1, R = n / C;
+    if (dy_colsum) {
+        if (dy_colsum->dtype != OXM_F32)
+            return fail(OXM_E_DTYPE_MISMATCH, "dtype mismatch: expected F32, got %s for dy_colsum in mse_loss",
+                        dtype_name(dy_colsum->dtype));
+        if (dy_colsum->ndim != 1 || dy_colsum->shape[0] != C || !is_contiguous(dy_colsum))
+            return fail(OXM_E_SHAPE_MISMATCH, "shape mismatch: expected [%lld], got %s for dy_colsum in mse_loss",
+                        (long long)C, shape_str(dy_colsum->ndim, dy_colsum->shape).c_str());
+        if (dy_colsum->device != y->device) return fail(OXM_E_DEVICE_MISMATCH, "device mismatch in mse_loss");
+    }
     DeviceGuard guard(y->device);
     if ((st = check_view_memory(y, "y", op)) != OXM_OK) return st;
     if ((st = check_view_memory(t, "target", op)) != OXM_OK) return st;
     if ((st = check_view_memory(dy, "dy", op)) != OXM_OK) return st;
     if ((st = check_view_memory(loss, "loss", op)) != OXM_OK) return st;
+    if (dy_colsum && (st = check_view_memory(dy_colsum, "dy_colsum", op)) != OXM_OK) return st;
     int es = dtype_size(y->dtype);
     hipStream_t s = (hipStream_t)stream;
     hipError_t e = oxm::launch_mse((const char *)y->data + y->offset * es, (const char *)t->data + t->offset * es,
-                                   (char *)dy->data + dy->offset * es, y->dtype, n, (float *)loss->data + loss->offset, s);
+                                   (char *)dy->data + dy->offset * es, y->dtype, R, C,
+                                   (float *)loss->data + loss->offset,
+                                   dy_colsum ? (float *)dy_colsum->data + dy_colsum->offset : nullptr, s);
     if (e != hipSuccess) return hip_fail(e, op);
     return finish(s, op);
 }

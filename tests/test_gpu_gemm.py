@@ -225,6 +225,69 @@ def test_dgelu_epilogue(hip, dtype):
     assert_close(to_f32(c), refw, spec_tolerance(dtype, k), "dgelu")
 
 
+def _check_colsum(cs: ox.Tensor, out: np.ndarray, what: str):
+    """The fused column sums against float64 sums of the stored output, under
+    the f32 summation bound rows * 2^-24 * sum |x| (plus a tiny floor)."""
+    x = np.asarray(out, np.float64).reshape(-1, out.shape[-1])
+    ref = x.sum(0)
+    bound = x.shape[0] * 2.0 ** -24 * np.abs(x).sum(0) + 1e-30
+    got = cs.to_numpy().astype(np.float64)
+    assert got.shape == ref.shape, what
+    worst = float(np.max(np.abs(got - ref) / bound))
+    assert worst <= 1.0, f"{what}: column sum off by {worst:.3g} x the f32 summation bound"
+
+
+@pytest.mark.parametrize("case", ["f32", "f32_ragged", "bf16_dgelu", "bf16_gelu_bf16out", "f32_batched",
+                                  "bf16_256tiles"])
+def test_epilogue_column_sums(hip, case):
+    """colsum = sums over rows (and batches) of the output as stored."""
+    rng = np.random.default_rng(41)
+    d = ox.Device.rocm(0)
+    kw = {}
+    if case in ("f32", "f32_ragged"):
+        m, k, n = (130, 96, 200) if case == "f32" else (77, 45, 131)
+        a = contiguous_operand(F32, rng.normal(0, 1, (m, k)))
+        b = contiguous_operand(F32, rng.normal(0, 1, (k, n)))
+        odt = F32
+    elif case == "bf16_dgelu":
+        m, k, n = 200, 128, 264
+        a = contiguous_operand(BF16, rng.normal(0, 1, (m, k)))
+        b = make_operand(BF16, "col", k, n, 43, "b")
+        zbuf = host_buffer(BF16, rng.normal(0, 1, m * n).astype(np.float32)).reshape(m, n)
+        kw = dict(act=ox.ACT_DGELU, aux=ox.Tensor.from_numpy(zbuf, d, BF16))
+        odt = BF16
+    elif case == "bf16_gelu_bf16out":
+        m, k, n = 136, 64, 200
+        a = contiguous_operand(BF16, rng.normal(0, 1, (m, k)))
+        b = contiguous_operand(BF16, rng.normal(0, 1, (k, n)))
+        bias = ox.Tensor.from_numpy(host_buffer(BF16, rng.normal(0, 1, n).astype(np.float32)), d, BF16)
+        kw = dict(bias=bias, act=ox.ACT_GELU, aux=ox.Tensor.empty((m, n), BF16, d))
+        odt = BF16
+    elif case == "f32_batched":
+        m, k, n = 37, 40, 45
+        a = Operand(F32, host_buffer(F32, rng.normal(0, 1, 3 * m * k).astype(np.float32)), (3, m, k),
+                    (m * k, k, 1))
+        b = contiguous_operand(F32, rng.normal(0, 1, (k, n)))
+        odt = F32
+    else:  # 256x256 direct-to-LDS tiles
+        m, k, n = 4096, 128, 4096
+        a = contiguous_operand(BF16, rng.normal(0, 1, (m, k)))
+        b = make_operand(BF16, "col", k, n, 44, "b")
+        odt = BF16
+    log(f"colsum {case}")
+    cs = ox.Tensor.empty((n,), F32, d)
+    c = hip.matmul(a.dev, b.dev, out_dtype=odt, colsum=cs, **kw)
+    _check_colsum(cs, to_f32(c), case)
+
+
+def test_epilogue_column_sums_of_no_rows(hip):
+    d = ox.Device.rocm(0)
+    cs = ox.Tensor.from_numpy(np.full(7, 5.0, np.float32), d)
+    c = hip.matmul(ox.Tensor.empty((0, 3), F32, d), ox.Tensor.empty((3, 7), F32, d), colsum=cs)
+    assert c.shape == (0, 7)
+    assert cs.to_numpy().tolist() == [0.0] * 7
+
+
 # ---- refusals that need device memory ------------------------------------------------
 
 def test_view_outside_allocation_is_refused(hip):

@@ -113,6 +113,31 @@ def gemm_checks(got, host, rows_per=6, seed=0):
     assert_close(got["dy"].to_numpy(), 2 * (yf - tf) / yf.size, TOL, "dY")
 
 
+@pytest.mark.parametrize("shape,dtype", [((300, 520), ox.DType.BF16), ((33, 37), ox.DType.F32),
+                                         ((2, 5, 64), ox.DType.F16), ((64, 256), ox.DType.F32)],
+                         ids=["bf16_vec", "f32_scalar", "f16_rank3", "f32_vec"])
+def test_mse_with_column_sums(hip, shape, dtype):
+    """loss, dy and the column sums of dy (the producing layer's bias
+    gradient) from one pass, against float64 on the host."""
+    from tests.parity import host_buffer
+    rng = np.random.default_rng(51)
+    n = int(np.prod(shape))
+    ybuf = host_buffer(dtype, rng.normal(0, 1, n).astype(np.float32)).reshape(shape)
+    tbuf = host_buffer(dtype, rng.normal(0, 1, n).astype(np.float32)).reshape(shape)
+    dev = ox.Device.rocm(0)
+    y, t = ox.Tensor.from_numpy(ybuf, dev, dtype), ox.Tensor.from_numpy(tbuf, dev, dtype)
+    cs = ox.Tensor.empty((shape[-1],), ox.DType.F32, dev)
+    loss, dy = hip.mse_loss_grad(y, t, dy_colsum=cs)
+    yf, tf = y.to_numpy().astype(np.float64), t.to_numpy().astype(np.float64)
+    loss_ref = np.mean((yf - tf) ** 2)
+    assert abs(float(loss.to_numpy()[0]) - loss_ref) <= 1e-5 * loss_ref
+    dyg = dy.to_numpy().astype(np.float64)
+    assert_close(dyg, 2 * (yf - tf) / n, TOL if dtype != ox.DType.F32 else 1e-6, "dy")
+    x = dyg.reshape(-1, shape[-1])
+    bound = x.shape[0] * 2.0 ** -24 * np.abs(x).sum(0) + 1e-30
+    assert np.all(np.abs(cs.to_numpy() - x.sum(0)) <= bound), "column sums of dy"
+
+
 def test_mlp_small_per_gemm(hip):
     host, T, model, x = build(256, 512, 2048, 8)
     got = intermediates(model, x, T["t"])
