@@ -199,6 +199,43 @@ def time_mlp(steps: int, warmup: int):
             "loss": float(loss.t.to_numpy()[0])}
 
 
+def time_vendor(kind: str, steps: int, warmup: int) -> dict:
+    """torch.matmul (hipBLASLt) on the same shapes, input dtypes and layout
+    (bf16: B a transposed view of an [N, K] buffer).  torch returns bf16 for
+    bf16 inputs, so its C is half the bytes of this backend's f32 C."""
+    import torch
+    dev = "cuda:0"
+    g = torch.Generator(device=dev).manual_seed(1)
+    if kind == "bf16":
+        n = 8192
+        a = (torch.randn(n, n, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        b = (torch.randn(n, n, device=dev, generator=g) * 0.02).to(torch.bfloat16).t()
+        flops = 2.0 * n ** 3
+    elif kind == "f32":
+        n = 4096
+        a = torch.randn(n, n, device=dev, generator=g)
+        b = torch.randn(n, n, device=dev, generator=g)
+        flops = 2.0 * n ** 3
+    else:
+        raise SystemExit("--vendor times the f32 and bf16 workloads")
+    for _ in range(warmup):
+        c = torch.matmul(a, b)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < WARMUP_S:
+        c = torch.matmul(a, b)
+        torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        c = torch.matmul(a, b)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / steps
+    del c
+    return {"vendor": "torch.matmul (hipBLASLt), black box", "workload": kind, "out_dtype": str(a.dtype),
+            "ms_per_launch": round(ms, 4), "TFLOP/s": round(flops / ms / 1e9, 1)}
+
+
 def host_cpu() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -354,6 +391,9 @@ def main():
                     help="f32 / bf16 (the headline configurations) or c1 / c2odd / c4 time one GEMM; mlp times "
                          "the MLP step alone (for profiling)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the extra workload")
+    ap.add_argument("--vendor", action="store_true",
+                    help="time torch.matmul (the vendor library, hipBLASLt, run as a black box) on the same "
+                         "operands and layout instead of this backend: a reference ceiling, not the metric")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB device copy (10x), the reference for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE scaling")
@@ -375,6 +415,9 @@ def main():
 
     if args.workload == "mlp":
         print(json.dumps({"mlp": time_mlp(args.steps, args.warmup)}), flush=True)
+        return
+    if args.vendor:
+        print(json.dumps(time_vendor(args.workload, args.steps, args.warmup)), flush=True)
         return
     main_kind = args.workload
     res = time_gpu(main_kind, args.steps, args.warmup)
