@@ -236,6 +236,57 @@ def time_vendor(kind: str, steps: int, warmup: int) -> dict:
             "ms_per_launch": round(ms, 4), "TFLOP/s": round(flops / ms / 1e9, 1)}
 
 
+def time_ops(steps: int = 20) -> dict:
+    """The HBM-bound ops of the rest of the Backend at [8192, 8192]: bytes
+    moved (one read of each input element, one write of each output
+    element) per launch / launch time, against the 8 TB/s HBM peak."""
+    import torch
+    import oxmera_amd as ox
+    ox.init()
+    dev = ox.Device.rocm(0)
+    be = ox.backend_for(dev)
+    n = 8192
+    rng = np.random.default_rng(99)
+    a = ox.Tensor.from_numpy(rng.standard_normal((n, n), dtype=np.float32), dev)
+    b = ox.Tensor.from_numpy(rng.standard_normal((n, n), dtype=np.float32), dev)
+    hb = ox.Tensor.from_numpy(ox.f32_to_bf16_bits(rng.standard_normal((n, n), dtype=np.float32)), dev, ox.DType.BF16)
+    ts = torch.cuda.Stream()
+    s = ts.cuda_stream
+    cases = {
+        "add f32 [8192,8192] + [8192,8192]": (lambda: be.add(a, b, stream=s), 3 * n * n * 4),
+        "add f32 [8192,8192] + [8192] (broadcast row)": (None, 2 * n * n * 4 + n * 4),
+        "exp bf16 [8192,8192]": (lambda: be.exp(hb, stream=s), 2 * n * n * 2),
+        "contiguous of a transposed bf16 [8192,8192] view": (lambda: be.contiguous(hb.permute([1, 0]), stream=s),
+                                                             2 * n * n * 2),
+        "sum f32 [8192,8192] over axis 0": (lambda: be.sum(a, [0], stream=s), n * n * 4 + n * 4),
+        "sum f32 [8192,8192] over axis 1": (lambda: be.sum(a, [1], stream=s), n * n * 4 + n * 4),
+        "max f32 [8192,8192] over all axes": (lambda: be.max(a, [], stream=s), n * n * 4),
+    }
+    row = ox.Tensor.from_numpy(rng.standard_normal(n, dtype=np.float32), dev)
+    cases["add f32 [8192,8192] + [8192] (broadcast row)"] = (lambda: be.add(a, row, stream=s), 2 * n * n * 4 + n * 4)
+    col = ox.Tensor.from_numpy(ox.f32_to_bf16_bits(rng.standard_normal((n, 1), dtype=np.float32)), dev, ox.DType.BF16)
+    cases["mul bf16 [8192,8192] * [8192,1] (broadcast column)"] = (lambda: be.mul(hb, col, stream=s),
+                                                                  2 * n * n * 2 + n * 2)
+    cases["sum bf16 [8192,8192] over axis 1"] = (lambda: be.sum(hb, [1], stream=s), n * n * 2 + n * 2)
+    out = {}
+    with torch.cuda.stream(ts):
+        for name, (fn, nbytes) in cases.items():
+            w0 = time.perf_counter()
+            while time.perf_counter() - w0 < 0.1:
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(ts)
+            for _ in range(steps):
+                fn()
+            e1.record(ts)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / steps
+            out[name] = {"ms": round(ms, 4), "GB/s": round(nbytes / ms / 1e6, 1),
+                         "frac_of_8TB/s": round(nbytes / ms / 1e6 / 8000.0, 3)}
+    return out
+
+
 def host_cpu() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -387,7 +438,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=["f32", "bf16", "mlp", "c1", "c2odd", "c4"], default="f32",
+    ap.add_argument("--workload", choices=["f32", "bf16", "mlp", "ops", "c1", "c2odd", "c4"], default="f32",
                     help="f32 / bf16 (the headline configurations) or c1 / c2odd / c4 time one GEMM; mlp times "
                          "the MLP step alone (for profiling)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the extra workload")
@@ -415,6 +466,9 @@ def main():
 
     if args.workload == "mlp":
         print(json.dumps({"mlp": time_mlp(args.steps, args.warmup)}), flush=True)
+        return
+    if args.workload == "ops":
+        print(json.dumps({"ops": time_ops(args.steps)}), flush=True)
         return
     if args.vendor:
         print(json.dumps(time_vendor(args.workload, args.steps, args.warmup)), flush=True)
@@ -451,6 +505,7 @@ def main():
         for other in others:
             line["extra"][other] = extra_line(other, args.steps, args.warmup)
         line["extra"]["mlp"] = time_mlp(max(3, args.steps // 10), 2)
+        line["extra"]["ops"] = time_ops()
     print(json.dumps(line), flush=True)
 
 

@@ -157,6 +157,40 @@ oxm_status oxm_sum_rows(const oxm_view *x, const oxm_view *out, void *stream);
 oxm_status oxm_mse_loss_grad(const oxm_view *y, const oxm_view *t, const oxm_view *loss, const oxm_view *dy,
                              const oxm_view *dy_colsum, void *stream);
 
+/* UnaryOps (crates/oxmera-ops/src/lib.rs:27-37): out = op(x) elementwise.
+ * x: any strided view of F32/F64/BF16/F16 on a HIP device; out: a contiguous
+ * view of x's shape and dtype ("a fresh contiguous tensor", :16-17).  exp
+ * and ln follow the device's IEEE-754 float functions (ln of a negative is
+ * NaN, of zero -inf). */
+typedef enum { OXM_UN_NEG = 0, OXM_UN_EXP = 1, OXM_UN_LN = 2, OXM_UN_ABS = 3 } oxm_unary_op;
+oxm_status oxm_unary(int32_t op, const oxm_view *x, const oxm_view *out, void *stream);
+
+/* BinaryOps (crates/oxmera-ops/src/lib.rs:39-50): out = a op b with NumPy
+ * broadcasting (crates/oxmera-core/src/shape.rs:45-58; BroadcastIncompatible
+ * otherwise).  a, b: same dtype (F32/F64/BF16/F16) and device, any strides;
+ * out: contiguous, the broadcast shape.  Float division follows IEEE-754. */
+typedef enum { OXM_BIN_ADD = 0, OXM_BIN_SUB = 1, OXM_BIN_MUL = 2, OXM_BIN_DIV = 3 } oxm_binary_op;
+oxm_status oxm_binary(int32_t op, const oxm_view *a, const oxm_view *b, const oxm_view *out, void *stream);
+
+/* ReduceOps (crates/oxmera-ops/src/lib.rs:61-69): sum or max over `axes`,
+ * removing them from the shape; naxes == 0 means every axis (a rank-0
+ * result).  Accumulation in f32 (f64 for F64), one rounding to the output
+ * dtype, a fixed combination order (results do not depend on scheduling).
+ * max propagates NaN and refuses an empty reduced extent (ShapeMismatch:
+ * "there is no identity to invent").  oxm_reduce_infer gives the output
+ * shape; out must be contiguous with it and x's dtype. */
+typedef enum { OXM_RED_SUM = 0, OXM_RED_MAX = 1 } oxm_reduce_op;
+oxm_status oxm_reduce_infer(const oxm_view *x, const int32_t *axes, int32_t naxes, int32_t *out_ndim,
+                            int64_t *out_shape);
+oxm_status oxm_reduce(int32_t op, const oxm_view *x, const int32_t *axes, int32_t naxes, const oxm_view *out,
+                      void *stream);
+
+/* Tensor::contiguous's copy (crates/oxmera-tensor/src/tensor.rs:86-90):
+ * dst = src element by element, bits unchanged.  Same shape and dtype, same
+ * HIP device; src any strides, dst any strides that do not repeat elements
+ * (a contiguous dst gives contiguous()). */
+oxm_status oxm_copy_view(const oxm_view *src, const oxm_view *dst, void *stream);
+
 /* Storage for device tensors (crates/oxmera-tensor/src/storage.rs:12-32,
  * "GPU variants hold opaque backend handles", :19-24). */
 oxm_status oxm_alloc(int32_t device, size_t bytes, void **out);

@@ -33,6 +33,10 @@ ACT_NONE = 0
 ACT_GELU = 1
 ACT_DGELU = 2
 
+UN_NEG, UN_EXP, UN_LN, UN_ABS = 0, 1, 2, 3
+BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV = 0, 1, 2, 3
+RED_SUM, RED_MAX = 0, 1
+
 
 class OxmView(C.Structure):
     _fields_ = [
@@ -71,6 +75,13 @@ _PROTOS = {
     "oxm_sum_rows": (C.c_int, [C.POINTER(OxmView), C.POINTER(OxmView), C.c_void_p]),
     "oxm_mse_loss_grad": (C.c_int, [C.POINTER(OxmView), C.POINTER(OxmView), C.POINTER(OxmView),
                                     C.POINTER(OxmView), C.POINTER(OxmView), C.c_void_p]),
+    "oxm_unary": (C.c_int, [C.c_int32, C.POINTER(OxmView), C.POINTER(OxmView), C.c_void_p]),
+    "oxm_binary": (C.c_int, [C.c_int32, C.POINTER(OxmView), C.POINTER(OxmView), C.POINTER(OxmView), C.c_void_p]),
+    "oxm_reduce_infer": (C.c_int, [C.POINTER(OxmView), C.POINTER(C.c_int32), C.c_int32, C.POINTER(C.c_int32),
+                                   C.POINTER(C.c_int64)]),
+    "oxm_reduce": (C.c_int, [C.c_int32, C.POINTER(OxmView), C.POINTER(C.c_int32), C.c_int32, C.POINTER(OxmView),
+                             C.c_void_p]),
+    "oxm_copy_view": (C.c_int, [C.POINTER(OxmView), C.POINTER(OxmView), C.c_void_p]),
     "oxm_alloc": (C.c_int, [C.c_int32, C.c_size_t, C.POINTER(C.c_void_p)]),
     "oxm_free": (C.c_int, [C.c_int32, C.c_void_p]),
     "oxm_copy": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_size_t, C.c_void_p]),

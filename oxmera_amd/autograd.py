@@ -67,7 +67,7 @@ class _LinearNode:
             # dW = x^T . dz  (x^T is a stride view)
             _set_grad(self.w, be.matmul(x2.transpose_last(), dz2, out_dtype=DType.F32), False)
         if self.wants_db():
-            _set_grad(self.b, self.db if self.db is not None else be.sum(dz2, [0]), False)
+            _set_grad(self.b, self.db if self.db is not None else be.sum_rows_f32(dz2), False)
         if self.x.requires_grad:
             prod = self.x.node
             fuse = isinstance(prod, _LinearNode) and prod.act == _lib.ACT_GELU

@@ -5,12 +5,13 @@ Mirrors:
     ``device()`` and ``name()``;
   - ``MatmulOps::matmul`` (crates/oxmera-ops/src/lib.rs:52-59), the hot path,
     served by ``oxm_gemm`` on gfx950;
-  - ``ReduceOps::sum`` (ops/src/lib.rs:61-69) for axis 0 of a rank-2 tensor
-    (the bias gradient), served by ``oxm_sum_rows``;
+  - ``UnaryOps`` / ``BinaryOps`` (ops/src/lib.rs:27-50) by ``oxm_unary`` /
+    ``oxm_binary`` (NumPy broadcasting), ``ReduceOps::sum`` / ``max``
+    (ops/src/lib.rs:61-69) by ``oxm_reduce``, all for F32/F64/BF16/F16;
+    other dtypes are ``UnsupportedDType`` (typed, never a panic);
+  - ``Tensor::contiguous`` (tensor/src/tensor.rs:86-90) by ``oxm_copy_view``;
   - ``backend_for`` / ``register_backend`` (runtime/src/lib.rs:36-53): an
     unregistered device is ``BackendUnavailable``, never a crash.
-Op families this backend does not carry raise ``NotImplementedOp``
-(``Error::NotImplemented``, core/src/error.rs:92-101), never ``todo!``.
 """
 from __future__ import annotations
 
@@ -79,37 +80,73 @@ class HipBackend:
         return out
 
     # ---- ReduceOps ----
+    def _reduce(self, op: int, a: Tensor, axes: Sequence[int], stream) -> Tensor:
+        ax = (C.c_int32 * max(1, len(axes)))(*[int(x) for x in axes])
+        v = a.abi_view()
+        nd = C.c_int32(0)
+        shp = (C.c_int64 * _lib.MAX_DIMS)()
+        check(_lib.lib().oxm_reduce_infer(C.byref(v), ax, len(axes), C.byref(nd), shp))
+        out = Tensor.empty(tuple(shp[i] for i in range(nd.value)), a.dtype, a.device)
+        o = out.abi_view()
+        check(_lib.lib().oxm_reduce(op, C.byref(v), ax, len(axes), C.byref(o), self._s(stream)))
+        return out
+
     def sum(self, a: Tensor, axes: Sequence[int], *, stream: int | None = None) -> Tensor:
-        if a.ndim != 2 or list(axes) != [0]:
-            raise NotImplementedOp(f"sum is not implemented for rank {a.ndim} over axes {list(axes)} "
-                                   "(hip backend: rank-2, axis 0)")
+        """Sum over ``axes``, removing them; empty ``axes`` = all (a rank-0 result)."""
+        return self._reduce(_lib.RED_SUM, a, axes, stream)
+
+    def max(self, a: Tensor, axes: Sequence[int], *, stream: int | None = None) -> Tensor:
+        """Maximum over ``axes``; an empty reduced extent is a typed error."""
+        return self._reduce(_lib.RED_MAX, a, axes, stream)
+
+    def sum_rows_f32(self, a: Tensor, *, stream: int | None = None) -> Tensor:
+        """Column sums of a rank-2 tensor with an F32 result whatever a's dtype
+        (the bias gradient of a Linear layer when no producer formed it)."""
         out = Tensor.empty((a.shape[1],), DType.F32, a.device)
         x, o = a.abi_view(), out.abi_view()
         check(_lib.lib().oxm_sum_rows(C.byref(x), C.byref(o), self._s(stream)))
         return out
 
-    def max(self, a: Tensor, axes: Sequence[int]) -> Tensor:
-        raise NotImplementedOp("max is not implemented for the hip backend")
+    # ---- UnaryOps / BinaryOps ----
+    def _unary(self, op: int, a: Tensor, stream=None) -> Tensor:
+        out = Tensor.empty(a.shape, a.dtype, a.device)
+        x, o = a.abi_view(), out.abi_view()
+        check(_lib.lib().oxm_unary(op, C.byref(x), C.byref(o), self._s(stream)))
+        return out
 
-    # ---- UnaryOps / BinaryOps (not carried by this backend) ----
-    def _absent(self, op: str):
-        raise NotImplementedOp(f"{op} is not implemented for the hip backend")
+    def _binary(self, op: int, lhs: Tensor, rhs: Tensor, stream=None) -> Tensor:
+        from .core import broadcast_shapes
+        out = Tensor.empty(tuple(broadcast_shapes(lhs.shape, rhs.shape)), lhs.dtype, lhs.device)
+        x, y, o = lhs.abi_view(), rhs.abi_view(), out.abi_view()
+        check(_lib.lib().oxm_binary(op, C.byref(x), C.byref(y), C.byref(o), self._s(stream)))
+        return out
 
-    def neg(self, a): self._absent("neg")
+    def neg(self, a, *, stream=None): return self._unary(_lib.UN_NEG, a, stream)
 
-    def exp(self, a): self._absent("exp")
+    def exp(self, a, *, stream=None): return self._unary(_lib.UN_EXP, a, stream)
 
-    def ln(self, a): self._absent("ln")
+    def ln(self, a, *, stream=None): return self._unary(_lib.UN_LN, a, stream)
 
-    def abs(self, a): self._absent("abs")
+    def abs(self, a, *, stream=None): return self._unary(_lib.UN_ABS, a, stream)
 
-    def add(self, lhs, rhs): self._absent("add")
+    def add(self, lhs, rhs, *, stream=None): return self._binary(_lib.BIN_ADD, lhs, rhs, stream)
 
-    def sub(self, lhs, rhs): self._absent("sub")
+    def sub(self, lhs, rhs, *, stream=None): return self._binary(_lib.BIN_SUB, lhs, rhs, stream)
 
-    def mul(self, lhs, rhs): self._absent("mul")
+    def mul(self, lhs, rhs, *, stream=None): return self._binary(_lib.BIN_MUL, lhs, rhs, stream)
 
-    def div(self, lhs, rhs): self._absent("div")
+    def div(self, lhs, rhs, *, stream=None): return self._binary(_lib.BIN_DIV, lhs, rhs, stream)
+
+    # ---- Tensor::contiguous ----
+    def contiguous(self, a: Tensor, *, stream: int | None = None) -> Tensor:
+        """a's elements in logical order in fresh contiguous storage; a itself
+        (sharing storage) when already contiguous (tensor.rs:86-90)."""
+        if a.layout.is_contiguous():
+            return a
+        out = Tensor.empty(a.shape, a.dtype, a.device)
+        x, o = a.abi_view(), out.abi_view()
+        check(_lib.lib().oxm_copy_view(C.byref(x), C.byref(o), self._s(stream)))
+        return out
 
     # ---- loss (MSE and its gradient in one pass) ----
     def mse_loss_grad(self, y: Tensor, t: Tensor, *, dy_colsum: Tensor | None = None,

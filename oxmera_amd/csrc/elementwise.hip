@@ -1,0 +1,655 @@
+// elementwise.hip -- the rest of oxmera's Backend on gfx950: UnaryOps,
+// BinaryOps (NumPy broadcasting), ReduceOps (sum / max over axes) and the
+// strided copy behind Tensor::contiguous (crates/oxmera-ops/src/lib.rs:27-69,
+// crates/oxmera-tensor/src/tensor.rs:86-90).
+//
+// All of these are HBM-bound: one read of each input element, one write of
+// each output element.  Operands are strided views (element strides, may be
+// zero for broadcast dims or negative); outputs are contiguous.  The host
+// collapses dimensions that are contiguous with each other, so most views
+// reach the kernels as one or two dims.  Contiguous same-shape operands take
+// a 16-byte-per-lane path; everything else decodes coordinates once per run
+// of consecutive elements along the innermost dimension.
+//
+// Reductions accumulate in f32 (f64 for F64 input) and round once.  Two
+// coalesced schedules: rows (an output's reduced elements contiguous: a
+// block walks them) and columns (consecutive outputs contiguous: a thread per
+// output walks the reduced elements); both keep several loads in flight per
+// thread and may split the reduced range over blocks, writing partials to a
+// workspace that a second pass combines in a fixed order -- no atomics, so
+// results do not depend on scheduling.  Other layouts: a thread per output.
+#include "elementwise_launch.hpp"
+#include "gemm_kernels.hpp"
+
+namespace oxm {
+
+namespace {
+
+// ---- element access ----------------------------------------------------------
+
+template <int DT>
+struct El;
+template <>
+struct El<kDtF32> {
+    using Acc = float;
+    __device__ static float load(const void *p, int64_t i) { return ((const float *)p)[i]; }
+    __device__ static void store(void *p, int64_t i, float v) { ((float *)p)[i] = v; }
+};
+template <>
+struct El<kDtBF16> {
+    using Acc = float;
+    __device__ static float load(const void *p, int64_t i) { return bf16_bits_to_f32(((const uint16_t *)p)[i]); }
+    __device__ static void store(void *p, int64_t i, float v) { ((uint16_t *)p)[i] = f32_to_bf16_bits(v); }
+};
+template <>
+struct El<kDtF16> {
+    using Acc = float;
+    __device__ static float load(const void *p, int64_t i) { return f16_bits_to_f32(((const uint16_t *)p)[i]); }
+    __device__ static void store(void *p, int64_t i, float v) { ((uint16_t *)p)[i] = f32_to_f16_bits(v); }
+};
+template <>
+struct El<kDtF64> {
+    using Acc = double;
+    __device__ static double load(const void *p, int64_t i) { return ((const double *)p)[i]; }
+    __device__ static void store(void *p, int64_t i, double v) { ((double *)p)[i] = v; }
+};
+
+// The op is a template parameter: each kernel is straight-line code (a
+// run-time switch per element compiled to branchy code that mishandled one
+// of its cases).
+template <int OP, typename A>
+__device__ __forceinline__ A apply_unary(A x) {
+    if constexpr (OP == kUnNeg)
+        return -x;
+    else if constexpr (OP == kUnExp)
+        return exp(x);
+    else if constexpr (OP == kUnLn)
+        return log(x);
+    else
+        return fabs(x);
+}
+
+template <int OP, typename A>
+__device__ __forceinline__ A apply_binary(A a, A b) {
+    if constexpr (OP == kBinAdd)
+        return a + b;
+    else if constexpr (OP == kBinSub)
+        return a - b;
+    else if constexpr (OP == kBinMul)
+        return a * b;
+    else
+        return a / b;
+}
+
+// Offsets of element `i` (row-major over `shape`) in up to three strided
+// operands.
+struct Coord {
+    __device__ static void offsets(const EwShape &s, int64_t i, int64_t &o0, int64_t &o1, int64_t &o2) {
+        o0 = o1 = o2 = 0;
+        for (int d = s.ndim - 1; d >= 0; --d) {
+            const int64_t e = s.shape[d];
+            const int64_t c = i % e;
+            i /= e;
+            o0 += c * s.st[0][d];
+            o1 += c * s.st[1][d];
+            o2 += c * s.st[2][d];
+        }
+    }
+};
+
+// ---- elementwise: strided (runs of kRun along the innermost dim) --------------
+
+constexpr int kRun = 4;
+
+// Unary (NOPS = 1) or binary (NOPS = 2) over a strided iteration space; the
+// output is operand index 0 (contiguous), inputs 1 and 2.
+template <int DT, int NOPS, int OP>
+__global__ void __launch_bounds__(256) ew_strided(EwShape s, void *out, const void *x, const void *y) {
+    using A = typename El<DT>::Acc;
+    const int64_t inner = s.shape[s.ndim - 1];
+    const int64_t runs_per_row = (inner + kRun - 1) / kRun;
+    const int64_t rows = s.numel / inner;
+    const int64_t nruns = rows * runs_per_row;
+    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < nruns; r += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = r / runs_per_row, c0 = (r - row * runs_per_row) * kRun;
+        int64_t oo, ox, oy;
+        Coord::offsets(s, row * inner + c0, oo, ox, oy);
+        const int64_t si0 = s.st[0][s.ndim - 1], si1 = s.st[1][s.ndim - 1], si2 = s.st[2][s.ndim - 1];
+#pragma unroll
+        for (int k = 0; k < kRun; ++k) {
+            if (c0 + k >= inner) break;
+            const A a = El<DT>::load(x, ox + k * si1);
+            A v;
+            if constexpr (NOPS == 1)
+                v = apply_unary<OP, A>(a);
+            else
+                v = apply_binary<OP, A>(a, El<DT>::load(y, oy + k * si2));
+            El<DT>::store(out, oo + k * si0, v);
+        }
+    }
+}
+
+// ---- elementwise: contiguous, same shape (16 bytes per lane) -------------------
+
+template <int DT>
+__device__ __forceinline__ void ld16(const void *p, int64_t i, float (&v)[DT == kDtF32 ? 4 : 8]) {
+    const uint4 u = *(const uint4 *)((const char *)p + i * (DT == kDtF32 ? 4 : 2));
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    if constexpr (DT == kDtF32) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(w[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t h = (w[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+            v[e] = DT == kDtBF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+        }
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void st16(void *p, int64_t i, const float (&v)[DT == kDtF32 ? 4 : 8]) {
+    uint32_t w[4];
+    if constexpr (DT == kDtF32) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = __float_as_uint(v[e]);
+    } else {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t lo = DT == kDtBF16 ? f32_to_bf16_bits(v[2 * d]) : f32_to_f16_bits(v[2 * d]);
+            const uint32_t hi = DT == kDtBF16 ? f32_to_bf16_bits(v[2 * d + 1]) : f32_to_f16_bits(v[2 * d + 1]);
+            w[d] = lo | (hi << 16);
+        }
+    }
+    *(uint4 *)((char *)p + i * (DT == kDtF32 ? 4 : 2)) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// n is a multiple of the vector width; every pointer 16-byte aligned.
+template <int DT, int NOPS, int OP>
+__global__ void __launch_bounds__(256) ew_contig16(int64_t n, void *out, const void *x, const void *y) {
+    constexpr int V = DT == kDtF32 ? 4 : 8;
+    const int64_t nv = n / V;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < nv; j += (int64_t)gridDim.x * blockDim.x) {
+        float a[V], b[V];
+        ld16<DT>(x, j * V, a);
+        if constexpr (NOPS == 2) ld16<DT>(y, j * V, b);
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            if constexpr (NOPS == 1)
+                a[e] = apply_unary<OP, float>(a[e]);
+            else
+                a[e] = apply_binary<OP, float>(a[e], b[e]);
+        }
+        st16<DT>(out, j * V, a);
+    }
+}
+
+// Rows of vectors: every operand of stride 1 (a vector load) or 0 (one
+// element repeated) along the innermost dim; outer dims through strides.
+template <int DT, int NOPS, int OP>
+__global__ void __launch_bounds__(256) ew_inner16(EwShape s, void *out, const void *x, const void *y) {
+    constexpr int V = DT == kDtF32 ? 4 : 8;
+    const int L = s.ndim - 1;
+    const int64_t inner = s.shape[L], vpr = inner / V, nv = s.numel / V;
+    const bool xv = s.st[1][L] != 0, yv = s.st[2][L] != 0;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < nv; j += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = j / vpr, c = (j - row * vpr) * V;
+        int64_t oo, ox, oy;
+        Coord::offsets(s, row * inner, oo, ox, oy);
+        float a[V], b[V];
+        if (xv) {
+            ld16<DT>(x, ox + c, a);
+        } else {
+            const float v = El<DT>::load(x, ox);
+#pragma unroll
+            for (int e = 0; e < V; ++e) a[e] = v;
+        }
+        if constexpr (NOPS == 2) {
+            if (yv) {
+                ld16<DT>(y, oy + c, b);
+            } else {
+                const float v = El<DT>::load(y, oy);
+#pragma unroll
+                for (int e = 0; e < V; ++e) b[e] = v;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            if constexpr (NOPS == 1)
+                a[e] = apply_unary<OP, float>(a[e]);
+            else
+                a[e] = apply_binary<OP, float>(a[e], b[e]);
+        }
+        st16<DT>(out, oo + c, a);
+    }
+}
+
+// ---- strided copy (bits unchanged) ------------------------------------------------
+
+template <typename U>
+__global__ void __launch_bounds__(256) copy_strided(EwShape s, U *dst, const U *src) {
+    const int64_t inner = s.shape[s.ndim - 1];
+    const int64_t runs_per_row = (inner + kRun - 1) / kRun;
+    const int64_t nruns = s.numel / inner * runs_per_row;
+    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < nruns; r += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = r / runs_per_row, c0 = (r - row * runs_per_row) * kRun;
+        int64_t od, os, unused;
+        Coord::offsets(s, row * inner + c0, od, os, unused);
+        const int64_t sd = s.st[0][s.ndim - 1], ss = s.st[1][s.ndim - 1];
+#pragma unroll
+        for (int k = 0; k < kRun; ++k) {
+            if (c0 + k >= inner) break;
+            dst[od + k * sd] = src[os + k * ss];
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) copy_contig16(int64_t n16, uint4 *dst, const uint4 *src) {
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n16; j += (int64_t)gridDim.x * blockDim.x)
+        dst[j] = src[j];
+}
+
+// Transposing copy: the source is contiguous along dim p, the destination
+// along the innermost dim L.  A block moves a kTT x kTT tile of (p, L) for
+// one combination of the other ("batch") dims through LDS, reading along p
+// and writing along L, so both sides are coalesced.
+constexpr int kTT = 64;
+
+template <typename U>
+__global__ void __launch_bounds__(256) copy_transpose(EwShape s, int p, U *dst, const U *src) {
+    __shared__ U tile[kTT][kTT + 1];
+    const int L = s.ndim - 1;
+    const int64_t np_ = s.shape[p], nl = s.shape[L];
+    const int64_t tiles_p = (np_ + kTT - 1) / kTT, tiles_l = (nl + kTT - 1) / kTT;
+    int64_t b = blockIdx.x;
+    const int64_t tl = b % tiles_l;
+    b /= tiles_l;
+    const int64_t tp = b % tiles_p;
+    b /= tiles_p;
+    int64_t od = 0, os = 0;  // batch offsets, dims other than p and L
+    for (int d = L - 1; d >= 0; --d) {
+        if (d == p) continue;
+        const int64_t c = b % s.shape[d];
+        b /= s.shape[d];
+        od += c * s.st[0][d];
+        os += c * s.st[1][d];
+    }
+    const int64_t p0 = tp * kTT, l0 = tl * kTT;
+    const int tx = threadIdx.x % kTT, ty = threadIdx.x / kTT;
+    const int64_t sl = s.st[1][L], dp = s.st[0][p];
+#pragma unroll
+    for (int k = 0; k < kTT / 4; ++k) {
+        const int j = ty + 4 * k;
+        if (p0 + tx < np_ && l0 + j < nl) tile[j][tx] = src[os + (p0 + tx) + (l0 + j) * sl];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kTT / 4; ++k) {
+        const int i = ty + 4 * k;
+        if (p0 + i < np_ && l0 + tx < nl) dst[od + (p0 + i) * dp + (l0 + tx)] = tile[tx][i];
+    }
+}
+
+// ---- reductions -------------------------------------------------------------------
+
+// Reduction geometry: the output's (kept) dims and the reduced dims, each
+// with the input's strides.
+template <int OP, typename A>
+__device__ __forceinline__ A red_identity() {
+    return OP == kRedSum ? (A)0 : -(A)INFINITY;
+}
+
+template <int OP, typename A>
+__device__ __forceinline__ A red_combine(A acc, A v) {
+    if constexpr (OP == kRedSum) {
+        return acc + v;
+    } else {
+        // max with NaN propagation (a NaN anywhere makes the result NaN)
+        if (v != v || acc != acc) return v != v ? v : acc;
+        return v > acc ? v : acc;
+    }
+}
+
+__device__ __forceinline__ int64_t dims_offset(int n, const int64_t *shape, const int64_t *st, int64_t i) {
+    int64_t o = 0;
+    for (int d = n - 1; d >= 0; --d) {
+        const int64_t c = i % shape[d];
+        i /= shape[d];
+        o += c * st[d];
+    }
+    return o;
+}
+
+// Element r (row-major over the reduced dims) of output o's reduction.
+__device__ __forceinline__ int64_t red_offset(const RedGeom &g, int64_t r) {
+    return g.nr == 1 ? r * g.rst[0] : dims_offset(g.nr, g.rshape, g.rst, r);
+}
+
+constexpr int kRedU = 8;  // independent loads in flight per thread
+
+// Generic: one thread per output element, the reduced elements in order.
+template <int DT, int OP>
+__global__ void __launch_bounds__(256) reduce_per_thread(RedGeom g, const void *x, void *out) {
+    using A = typename El<DT>::Acc;
+    for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < g.n_out;
+         o += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t base = dims_offset(g.nk, g.kshape, g.kst, o);
+        A acc = red_identity<OP, A>();
+        for (int64_t r = 0; r < g.n_red; ++r) acc = red_combine<OP, A>(acc, (A)El<DT>::load(x, base + red_offset(g, r)));
+        El<DT>::store(out, o, acc);
+    }
+}
+
+// Rows: output o's reduced elements are contiguous in memory (one reduced
+// dim of stride 1).  Block (o, s) takes split s of the row; each thread
+// keeps kRedU independent partials so kRedU coalesced loads are in flight.
+// VEC: the loads are 16-byte vectors (the launcher has checked that every
+// row starts 16-byte aligned and n_red is a multiple of the vector); the
+// split size is then rounded up to a whole number of vectors.
+// Result to out (splits == 1) or to ws[o * splits + s].
+template <int DT, int OP, bool VEC>
+__global__ void __launch_bounds__(256) reduce_rows(RedGeom g, const void *x, void *out, typename El<DT>::Acc *ws,
+                                                   int splits) {
+    using A = typename El<DT>::Acc;
+    __shared__ A red[256];
+    const int64_t o = blockIdx.x / splits;
+    const int s = blockIdx.x % splits;
+    const int64_t base = dims_offset(g.nk, g.kshape, g.kst, o);
+    int64_t chunk = (g.n_red + splits - 1) / splits;
+    A acc[kRedU];
+#pragma unroll
+    for (int u = 0; u < kRedU; ++u) acc[u] = red_identity<OP, A>();
+    if constexpr (VEC) {
+        constexpr int V = DT == kDtF32 ? 4 : 8;
+        chunk = (chunk + V - 1) / V * V;
+        const int64_t r0 = s * chunk, r1 = r0 + chunk < g.n_red ? r0 + chunk : g.n_red;
+        for (int64_t r = r0 + threadIdx.x * V; r < r1; r += 256 * V * kRedU) {
+            float v[kRedU][V];
+#pragma unroll
+            for (int u = 0; u < kRedU; ++u) {
+                if (r + u * 256 * V < r1) {
+                    ld16<DT>(x, base + r + u * 256 * V, v[u]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) v[u][e] = red_identity<OP, A>();
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kRedU; ++u)
+#pragma unroll
+                for (int e = 0; e < V; ++e) acc[u] = red_combine<OP, A>(acc[u], v[u][e]);
+        }
+    } else {
+        const int64_t r0 = s * chunk, r1 = r0 + chunk < g.n_red ? r0 + chunk : g.n_red;
+        for (int64_t r = r0 + threadIdx.x; r < r1; r += 256 * kRedU) {
+            A v[kRedU];
+#pragma unroll
+            for (int u = 0; u < kRedU; ++u)
+                v[u] = r + u * 256 < r1 ? (A)El<DT>::load(x, base + r + u * 256) : red_identity<OP, A>();
+#pragma unroll
+            for (int u = 0; u < kRedU; ++u) acc[u] = red_combine<OP, A>(acc[u], v[u]);
+        }
+    }
+#pragma unroll
+    for (int u = 1; u < kRedU; ++u) acc[0] = red_combine<OP, A>(acc[0], acc[u]);
+    red[threadIdx.x] = acc[0];
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] = red_combine<OP, A>(red[threadIdx.x], red[threadIdx.x + w]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        if (splits == 1)
+            El<DT>::store(out, o, red[0]);
+        else
+            ws[o * splits + s] = red[0];
+    }
+}
+
+// Columns: consecutive outputs are consecutive in memory (the innermost kept
+// dim has stride 1), so a block of 256 threads takes 256 consecutive outputs
+// (coalesced) over split s of the reduced range, kRedU reduced elements in
+// flight per thread.  Result to out (splits == 1) or to ws[s * n_out + o].
+template <int DT, int OP>
+__global__ void __launch_bounds__(256) reduce_cols(RedGeom g, const void *x, void *out, typename El<DT>::Acc *ws,
+                                                   int splits) {
+    using A = typename El<DT>::Acc;
+    const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int s = blockIdx.y;
+    if (o >= g.n_out) return;
+    const int64_t base = dims_offset(g.nk, g.kshape, g.kst, o);
+    const int64_t chunk = (g.n_red + splits - 1) / splits;
+    const int64_t r0 = s * chunk, r1 = r0 + chunk < g.n_red ? r0 + chunk : g.n_red;
+    A acc[kRedU];
+#pragma unroll
+    for (int u = 0; u < kRedU; ++u) acc[u] = red_identity<OP, A>();
+    for (int64_t r = r0; r < r1; r += kRedU) {
+        A v[kRedU];
+#pragma unroll
+        for (int u = 0; u < kRedU; ++u) v[u] = r + u < r1 ? (A)El<DT>::load(x, base + red_offset(g, r + u)) : red_identity<OP, A>();
+#pragma unroll
+        for (int u = 0; u < kRedU; ++u) acc[u] = red_combine<OP, A>(acc[u], v[u]);
+    }
+#pragma unroll
+    for (int u = 1; u < kRedU; ++u) acc[0] = red_combine<OP, A>(acc[0], acc[u]);
+    if (splits == 1)
+        El<DT>::store(out, o, acc[0]);
+    else
+        ws[(int64_t)s * g.n_out + o] = acc[0];
+}
+
+// out[o] = the splits' partials combined, in a fixed order.  stride_o /
+// stride_s address ws[o * stride_o + s * stride_s].  A thread per output,
+// kRedU partials in flight.
+template <int DT, int OP>
+__global__ void __launch_bounds__(256) reduce_finish(const typename El<DT>::Acc *ws, int64_t n_out, int splits,
+                                                     int64_t stride_o, int64_t stride_s, void *out) {
+    using A = typename El<DT>::Acc;
+    for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < n_out; o += (int64_t)gridDim.x * blockDim.x) {
+        A acc[kRedU];
+#pragma unroll
+        for (int u = 0; u < kRedU; ++u) acc[u] = red_identity<OP, A>();
+        for (int s = 0; s < splits; s += kRedU) {
+            A v[kRedU];
+#pragma unroll
+            for (int u = 0; u < kRedU; ++u) v[u] = s + u < splits ? ws[o * stride_o + (s + u) * stride_s] : red_identity<OP, A>();
+#pragma unroll
+            for (int u = 0; u < kRedU; ++u) acc[u] = red_combine<OP, A>(acc[u], v[u]);
+        }
+#pragma unroll
+        for (int u = 1; u < kRedU; ++u) acc[0] = red_combine<OP, A>(acc[0], acc[u]);
+        El<DT>::store(out, o, acc[0]);
+    }
+}
+
+// The same with a block per output (few outputs, many splits): thread t
+// takes partials t, t + 256, ..., then a tree over the block.
+template <int DT, int OP>
+__global__ void __launch_bounds__(256) reduce_finish_block(const typename El<DT>::Acc *ws, int splits, int64_t stride_o,
+                                                           int64_t stride_s, void *out) {
+    using A = typename El<DT>::Acc;
+    __shared__ A red[256];
+    const int64_t o = blockIdx.x;
+    A acc = red_identity<OP, A>();
+    for (int s = threadIdx.x; s < splits; s += 256) acc = red_combine<OP, A>(acc, ws[o * stride_o + s * stride_s]);
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] = red_combine<OP, A>(red[threadIdx.x], red[threadIdx.x + w]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) El<DT>::store(out, o, red[0]);
+}
+
+// ---- dispatch helpers ------------------------------------------------------------
+
+unsigned grid_for(int64_t work) {
+    int64_t g = (work + 255) / 256;
+    if (g > 65536) g = 65536;
+    return (unsigned)(g < 1 ? 1 : g);
+}
+
+template <int DT, int NOPS, int OP>
+hipError_t ew_launch(const EwShape &s, void *out, const void *x, const void *y, int vec, hipStream_t st) {
+    if constexpr (DT != kDtF64) {
+        constexpr int V = DT == kDtF32 ? 4 : 8;
+        if (vec == kEwContig16) {
+            hipLaunchKernelGGL((ew_contig16<DT, NOPS, OP>), dim3(grid_for(s.numel / V)), dim3(256), 0, st, s.numel, out,
+                               x, y);
+            return hipGetLastError();
+        }
+        if (vec == kEwInner16) {
+            hipLaunchKernelGGL((ew_inner16<DT, NOPS, OP>), dim3(grid_for(s.numel / V)), dim3(256), 0, st, s, out, x, y);
+            return hipGetLastError();
+        }
+    }
+    const int64_t runs = s.numel / s.shape[s.ndim - 1] * ((s.shape[s.ndim - 1] + kRun - 1) / kRun);
+    hipLaunchKernelGGL((ew_strided<DT, NOPS, OP>), dim3(grid_for(runs)), dim3(256), 0, st, s, out, x, y);
+    return hipGetLastError();
+}
+
+template <int DT>
+hipError_t ew_dispatch(int nops, int op, const EwShape &s, void *out, const void *x, const void *y, int vec,
+                       hipStream_t st) {
+    if (s.numel == 0) return hipSuccess;
+    if (nops == 1) {
+        switch (op) {
+        case kUnNeg: return ew_launch<DT, 1, kUnNeg>(s, out, x, y, vec, st);
+        case kUnExp: return ew_launch<DT, 1, kUnExp>(s, out, x, y, vec, st);
+        case kUnLn: return ew_launch<DT, 1, kUnLn>(s, out, x, y, vec, st);
+        default: return ew_launch<DT, 1, kUnAbs>(s, out, x, y, vec, st);
+        }
+    }
+    switch (op) {
+    case kBinAdd: return ew_launch<DT, 2, kBinAdd>(s, out, x, y, vec, st);
+    case kBinSub: return ew_launch<DT, 2, kBinSub>(s, out, x, y, vec, st);
+    case kBinMul: return ew_launch<DT, 2, kBinMul>(s, out, x, y, vec, st);
+    default: return ew_launch<DT, 2, kBinDiv>(s, out, x, y, vec, st);
+    }
+}
+
+template <int DT, int OP>
+hipError_t red_launch(const RedGeom &g, const void *x, void *out, hipStream_t st) {
+    using A = typename El<DT>::Acc;
+    if (g.n_out == 0) return hipSuccess;
+    const bool rows = g.nr == 1 && g.rst[0] == 1 && g.n_red >= 256;
+    const bool cols = !rows && g.kst[g.nk - 1] == 1 && g.n_out >= 64 && g.n_red >= 2 * kRedU;
+    int64_t splits = 1;
+    if (rows) {
+        splits = 2048 / g.n_out;
+        const int64_t cap = g.n_red / 4096;  // >= 4096 elements per block
+        if (splits > cap) splits = cap;
+    } else if (cols) {
+        const int64_t col_blocks = (g.n_out + 255) / 256;
+        splits = 2048 / col_blocks;
+        const int64_t cap = g.n_red / 64;  // >= 64 reduced elements per thread
+        if (splits > cap) splits = cap;
+    } else {
+        hipLaunchKernelGGL((reduce_per_thread<DT, OP>), dim3(grid_for(g.n_out)), dim3(256), 0, st, g, x, out);
+        return hipGetLastError();
+    }
+    if (splits < 1) splits = 1;
+    A *ws = nullptr;
+    hipError_t e;
+    if (splits > 1 && (e = hipMallocAsync((void **)&ws, sizeof(A) * g.n_out * splits, st)) != hipSuccess) return e;
+    auto finish = [&](int64_t stride_o, int64_t stride_s) {
+        if (g.n_out <= 1024 && splits >= 64)
+            hipLaunchKernelGGL((reduce_finish_block<DT, OP>), dim3((unsigned)g.n_out), dim3(256), 0, st, ws, (int)splits,
+                               stride_o, stride_s, out);
+        else
+            hipLaunchKernelGGL((reduce_finish<DT, OP>), dim3(grid_for(g.n_out)), dim3(256), 0, st, ws, g.n_out,
+                               (int)splits, stride_o, stride_s, out);
+    };
+    if (rows) {
+        bool vec = false;
+        if constexpr (DT != kDtF64) {
+            constexpr int V = DT == kDtF32 ? 4 : 8;
+            vec = (uintptr_t)x % 16 == 0 && g.n_red % V == 0;
+            for (int d = 0; d < g.nk; ++d) vec = vec && g.kst[d] % V == 0;
+            if (vec)
+                hipLaunchKernelGGL((reduce_rows<DT, OP, true>), dim3((unsigned)(g.n_out * splits)), dim3(256), 0, st, g,
+                                   x, out, ws, (int)splits);
+        }
+        if (!vec)
+            hipLaunchKernelGGL((reduce_rows<DT, OP, false>), dim3((unsigned)(g.n_out * splits)), dim3(256), 0, st, g, x,
+                               out, ws, (int)splits);
+        if (splits > 1) finish(splits, (int64_t)1);
+    } else {
+        hipLaunchKernelGGL((reduce_cols<DT, OP>), dim3((unsigned)((g.n_out + 255) / 256), (unsigned)splits), dim3(256), 0,
+                           st, g, x, out, ws, (int)splits);
+        if (splits > 1) finish((int64_t)1, g.n_out);
+    }
+    e = hipGetLastError();
+    if (ws) {
+        hipError_t f = hipFreeAsync(ws, st);
+        if (e == hipSuccess) e = f;
+    }
+    return e;
+}
+
+template <int DT>
+hipError_t red_dispatch(int op, const RedGeom &g, const void *x, void *out, hipStream_t st) {
+    return op == kRedSum ? red_launch<DT, kRedSum>(g, x, out, st) : red_launch<DT, kRedMax>(g, x, out, st);
+}
+
+}  // namespace
+
+hipError_t launch_elementwise(int dtype, int nops, int op, const EwShape &s, void *out, const void *x, const void *y,
+                              int vec, hipStream_t st) {
+    switch (dtype) {
+    case kDtF32: return ew_dispatch<kDtF32>(nops, op, s, out, x, y, vec, st);
+    case kDtBF16: return ew_dispatch<kDtBF16>(nops, op, s, out, x, y, vec, st);
+    case kDtF16: return ew_dispatch<kDtF16>(nops, op, s, out, x, y, vec, st);
+    default: return ew_dispatch<kDtF64>(nops, op, s, out, x, y, vec, st);
+    }
+}
+
+hipError_t launch_copy(int elem_bytes, const EwShape &s, void *dst, const void *src, bool contig16, hipStream_t st) {
+    if (s.numel == 0) return hipSuccess;
+    if (contig16) {
+        const int64_t n16 = s.numel * elem_bytes / 16;
+        hipLaunchKernelGGL(copy_contig16, dim3(grid_for(n16)), dim3(256), 0, st, n16, (uint4 *)dst, (const uint4 *)src);
+        return hipGetLastError();
+    }
+    const int L = s.ndim - 1;
+    int p = -1;
+    if (s.ndim >= 2 && s.st[0][L] == 1 && s.st[1][L] != 1 && s.shape[L] >= 16)
+        for (int d = L - 1; d >= 0; --d)
+            if (s.st[1][d] == 1 && s.shape[d] >= 16) {
+                p = d;
+                break;
+            }
+    const int64_t blocks = p < 0 ? 0
+                                 : s.numel / (s.shape[p] * s.shape[L]) * ((s.shape[p] + kTT - 1) / kTT) *
+                                       ((s.shape[L] + kTT - 1) / kTT);
+    if (p >= 0 && blocks <= INT32_MAX) {
+        const dim3 g((unsigned)blocks);
+        switch (elem_bytes) {
+        case 1: hipLaunchKernelGGL(copy_transpose<uint8_t>, g, dim3(256), 0, st, s, p, (uint8_t *)dst, (const uint8_t *)src); break;
+        case 2: hipLaunchKernelGGL(copy_transpose<uint16_t>, g, dim3(256), 0, st, s, p, (uint16_t *)dst, (const uint16_t *)src); break;
+        case 4: hipLaunchKernelGGL(copy_transpose<uint32_t>, g, dim3(256), 0, st, s, p, (uint32_t *)dst, (const uint32_t *)src); break;
+        default: hipLaunchKernelGGL(copy_transpose<uint64_t>, g, dim3(256), 0, st, s, p, (uint64_t *)dst, (const uint64_t *)src); break;
+        }
+        return hipGetLastError();
+    }
+    const int64_t runs = s.numel / s.shape[L] * ((s.shape[L] + kRun - 1) / kRun);
+    const dim3 grid(grid_for(runs));
+    switch (elem_bytes) {
+    case 1: hipLaunchKernelGGL(copy_strided<uint8_t>, grid, dim3(256), 0, st, s, (uint8_t *)dst, (const uint8_t *)src); break;
+    case 2: hipLaunchKernelGGL(copy_strided<uint16_t>, grid, dim3(256), 0, st, s, (uint16_t *)dst, (const uint16_t *)src); break;
+    case 4: hipLaunchKernelGGL(copy_strided<uint32_t>, grid, dim3(256), 0, st, s, (uint32_t *)dst, (const uint32_t *)src); break;
+    default: hipLaunchKernelGGL(copy_strided<uint64_t>, grid, dim3(256), 0, st, s, (uint64_t *)dst, (const uint64_t *)src); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_reduce(int dtype, int op, const RedGeom &g, const void *x, void *out, hipStream_t st) {
+    switch (dtype) {
+    case kDtF32: return red_dispatch<kDtF32>(op, g, x, out, st);
+    case kDtBF16: return red_dispatch<kDtBF16>(op, g, x, out, st);
+    case kDtF16: return red_dispatch<kDtF16>(op, g, x, out, st);
+    default: return red_dispatch<kDtF64>(op, g, x, out, st);
+    }
+}
+
+}  // namespace oxm

@@ -1,0 +1,52 @@
+// elementwise_launch.hpp -- host <-> kernel interface of elementwise.hip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace oxm {
+
+constexpr int kDtF64 = 1;  // oxm_dtype F64 (F32 = 0, BF16 = 6, F16 = 7 are in gemm_kernels.hpp)
+
+enum UnaryOp : int { kUnNeg = 0, kUnExp = 1, kUnLn = 2, kUnAbs = 3 };
+enum BinaryOp : int { kBinAdd = 0, kBinSub = 1, kBinMul = 2, kBinDiv = 3 };
+enum ReduceOp : int { kRedSum = 0, kRedMax = 1 };
+
+constexpr int kEwMaxDims = 8;
+
+// A row-major iteration space over the output shape and, per operand
+// (0 = output, 1 and 2 = inputs), its element strides (0 on broadcast dims).
+struct EwShape {
+    int32_t ndim;  // >= 1
+    int64_t numel;
+    int64_t shape[kEwMaxDims];
+    int64_t st[3][kEwMaxDims];
+};
+
+// out[o] = reduce over the reduced dims; the output (kept dims, row-major)
+// is contiguous.  Strides are the input's.
+struct RedGeom {
+    int32_t nk, nr;  // nk >= 1 (a scalar output is one kept dim of extent 1), nr >= 1
+    int64_t n_out, n_red;
+    int64_t kshape[kEwMaxDims], kst[kEwMaxDims];
+    int64_t rshape[kEwMaxDims], rst[kEwMaxDims];
+};
+
+// Vector paths of an elementwise launch.  kEwContig16: every operand
+// contiguous over s (one dim), 16-byte aligned, numel a multiple of 16 bytes.
+// kEwInner16: every operand of stride 1 or 0 along the innermost dim (the
+// output 1), that extent a multiple of 16 bytes, stride-1 operands' vectors
+// 16-byte aligned.  kEwScalar: anything else.
+enum EwVec { kEwScalar = 0, kEwContig16 = 1, kEwInner16 = 2 };
+
+// nops 1: out = op(x); nops 2: out = op(x, y).  vec: an EwVec the caller has
+// checked s and the pointers against.
+hipError_t launch_elementwise(int dtype, int nops, int op, const EwShape &s, void *out, const void *x, const void *y,
+                              int vec, hipStream_t st);
+
+// Element copy of elem_bytes-sized elements from a strided view (operand 1)
+// to a strided destination (operand 0), bits unchanged.
+hipError_t launch_copy(int elem_bytes, const EwShape &s, void *dst, const void *src, bool contig16, hipStream_t st);
+
+hipError_t launch_reduce(int dtype, int op, const RedGeom &g, const void *x, void *out, hipStream_t st);
+
+}  // namespace oxm

@@ -13,9 +13,11 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/oxm.h"
 #include "gemm_args.hpp"
+#include "elementwise_launch.hpp"
 #include "gemm_launch.hpp"
 #include "glue_launch.hpp"
 
@@ -272,6 +274,95 @@ bool prefer_256_tiles(int64_t M, int64_t N, int64_t batch) {
 int env_int(const char *name, int dflt) {
     const char *v = getenv(name);
     return v && *v ? atoi(v) : dflt;
+}
+
+bool is_float_dtype(int dt) { return dt == OXM_F32 || dt == OXM_F64 || dt == OXM_BF16 || dt == OXM_F16; }
+
+// Row-major iteration space over `shape` for up to three operands (0 = the
+// output), dims of extent 1 dropped and neighbours merged where every
+// operand walks them as one (st[d] == st[d+1] * shape[d+1]).
+oxm::EwShape collapse(int nd, const int64_t *shape, const int64_t *const st[3], int nops) {
+    oxm::EwShape s{};
+    s.numel = 1;
+    for (int d = 0; d < nd; ++d) s.numel *= shape[d];
+    int n = 0;
+    for (int d = 0; d < nd; ++d) {
+        if (shape[d] == 1) continue;
+        bool merge = n > 0;
+        for (int o = 0; o < nops && merge; ++o) merge = s.st[o][n - 1] == st[o][d] * shape[d];
+        if (merge) {
+            s.shape[n - 1] *= shape[d];
+            for (int o = 0; o < nops; ++o) s.st[o][n - 1] = st[o][d];
+        } else {
+            s.shape[n] = shape[d];
+            for (int o = 0; o < nops; ++o) s.st[o][n] = st[o][d];
+            ++n;
+        }
+    }
+    if (n == 0) {  // every extent 1: one element
+        s.shape[0] = 1;
+        n = 1;
+    }
+    s.ndim = n;
+    return s;
+}
+
+// 16-byte path: every operand walks the space as one unit-stride run from a
+// 16-byte aligned address, and the run is a whole number of 16-byte chunks.
+bool contig16(const oxm::EwShape &s, int nops, const void *const ptr[3], int es) {
+    if (s.ndim != 1 || (s.numel * es) % 16 != 0) return false;
+    for (int o = 0; o < nops; ++o)
+        if (s.st[o][0] != 1 || ((uintptr_t)ptr[o] % 16) != 0) return false;
+    return true;
+}
+
+// Rows of 16-byte vectors: every operand is contiguous (stride 1) or
+// repeated (stride 0) along the innermost dim, the output contiguous; the
+// innermost extent a multiple of the vector, and every stride-1 operand's
+// vectors 16-byte aligned.  Covers broadcasts of rows and of columns.
+bool inner16(const oxm::EwShape &s, int nops, const void *const ptr[3], int es) {
+    if (es != 2 && es != 4) return false;
+    const int L = s.ndim - 1, V = 16 / es;
+    if (s.shape[L] % V != 0 || s.st[0][L] != 1) return false;
+    for (int o = 0; o < nops; ++o) {
+        if (s.st[o][L] == 0) continue;
+        if (s.st[o][L] != 1 || ((uintptr_t)ptr[o] % 16) != 0) return false;
+        for (int d = 0; d < L; ++d)
+            if (s.st[o][d] % V != 0) return false;
+    }
+    return true;
+}
+
+// Vector path for an elementwise launch (oxm::EwVec).
+int ew_vec(const oxm::EwShape &s, int nops, const void *const ptr[3], int es) {
+    if (contig16(s, nops, ptr, es)) return oxm::kEwContig16;
+    if (inner16(s, nops, ptr, es)) return oxm::kEwInner16;
+    return oxm::kEwScalar;
+}
+
+const char *unary_name(int op) {
+    static const char *n[] = {"neg", "exp", "ln", "abs"};
+    return op >= 0 && op < 4 ? n[op] : "unary";
+}
+const char *binary_name(int op) {
+    static const char *n[] = {"add", "sub", "mul", "div"};
+    return op >= 0 && op < 4 ? n[op] : "binary";
+}
+
+// The checks every elementwise output needs: dtype, shape, contiguity,
+// device, memory.
+oxm_status check_out(const oxm_view *out, int dtype, int nd, const int64_t *shape, int device, const char *op) {
+    if (out->dtype != dtype)
+        return fail(OXM_E_DTYPE_MISMATCH, "dtype mismatch: expected %s, got %s in %s (out)", dtype_name(dtype),
+                    dtype_name(out->dtype), op);
+    if (out->ndim != nd || (nd && memcmp(out->shape, shape, 8 * nd)))
+        return fail(OXM_E_SHAPE_MISMATCH, "shape mismatch: expected %s, got %s in %s", shape_str(nd, shape).c_str(),
+                    shape_str(out->ndim, out->shape).c_str(), op);
+    if (!is_contiguous(out)) return fail(OXM_E_NOT_IMPLEMENTED, "%s is not implemented for a non-contiguous output", op);
+    if (out->device != device)
+        return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s vs %s in %s", device_str(device).c_str(),
+                    device_str(out->device).c_str(), op);
+    return OXM_OK;
 }
 
 }  // namespace
@@ -606,6 +697,211 @@ oxm_status oxm_copy(void *dst, int32_t dst_device, const void *src, int32_t src_
     hipError_t e = s ? hipMemcpyAsync(dst, src, bytes, kind, s) : hipMemcpy(dst, src, bytes, kind);
     if (e != hipSuccess) return hip_fail(e, "copy");
     return ok();
+}
+
+oxm_status oxm_unary(int32_t op, const oxm_view *x, const oxm_view *out, void *stream) {
+    if (op < OXM_UN_NEG || op > OXM_UN_ABS) return fail(OXM_E_INVALID_ARGUMENT, "unary: unknown op %d", op);
+    const char *name = unary_name(op);
+    oxm_status st;
+    if ((st = check_view(x, "input", name)) != OXM_OK) return st;
+    if ((st = check_view(out, "out", name)) != OXM_OK) return st;
+    if (!is_float_dtype(x->dtype))
+        return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by %s", dtype_name(x->dtype), name);
+    if (x->device < 0) return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s is not a HIP device in %s",
+                                   device_str(x->device).c_str(), name);
+    if ((st = check_out(out, x->dtype, x->ndim, x->shape, x->device, name)) != OXM_OK) return st;
+    if (numel(x) == 0) return ok();
+    DeviceGuard guard(x->device);
+    if ((st = check_view_memory(x, "input", name)) != OXM_OK) return st;
+    if ((st = check_view_memory(out, "out", name)) != OXM_OK) return st;
+    const int es = dtype_size(x->dtype);
+    std::vector<int64_t> ost(x->ndim > 0 ? x->ndim : 1);
+    int64_t acc = 1;
+    for (int d = x->ndim - 1; d >= 0; --d) {
+        ost[d] = acc;
+        acc *= x->shape[d];
+    }
+    const int64_t *sts[3] = {ost.data(), x->strides, nullptr};
+    oxm::EwShape sh = collapse(x->ndim, x->shape, sts, 2);
+    void *po = (char *)out->data + out->offset * es;
+    const void *px = (const char *)x->data + x->offset * es;
+    const void *ptrs[3] = {po, px, nullptr};
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = oxm::launch_elementwise(x->dtype, 1, op, sh, po, px, nullptr, ew_vec(sh, 2, ptrs, es), s);
+    if (e != hipSuccess) return hip_fail(e, name);
+    return finish(s, name);
+}
+
+oxm_status oxm_binary(int32_t op, const oxm_view *a, const oxm_view *b, const oxm_view *out, void *stream) {
+    if (op < OXM_BIN_ADD || op > OXM_BIN_DIV) return fail(OXM_E_INVALID_ARGUMENT, "binary: unknown op %d", op);
+    const char *name = binary_name(op);
+    oxm_status st;
+    if ((st = check_view(a, "lhs", name)) != OXM_OK) return st;
+    if ((st = check_view(b, "rhs", name)) != OXM_OK) return st;
+    if ((st = check_view(out, "out", name)) != OXM_OK) return st;
+    if (a->dtype != b->dtype)
+        return fail(OXM_E_DTYPE_MISMATCH, "dtype mismatch: expected %s, got %s in %s", dtype_name(a->dtype),
+                    dtype_name(b->dtype), name);
+    if (!is_float_dtype(a->dtype))
+        return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by %s", dtype_name(a->dtype), name);
+    if (a->device != b->device)
+        return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s vs %s in %s", device_str(a->device).c_str(),
+                    device_str(b->device).c_str(), name);
+    if (a->device < 0) return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s is not a HIP device in %s",
+                                   device_str(a->device).c_str(), name);
+    int32_t nd = 0;
+    int64_t shape[OXM_MAX_DIMS];
+    if ((st = oxm_broadcast_shapes(a->ndim, a->shape, b->ndim, b->shape, &nd, shape)) != OXM_OK) return st;
+    if ((st = check_out(out, a->dtype, nd, shape, a->device, name)) != OXM_OK) return st;
+    int64_t n = 1;
+    for (int d = 0; d < nd; ++d) n *= shape[d];
+    if (n == 0) return ok();
+    DeviceGuard guard(a->device);
+    if ((st = check_view_memory(a, "lhs", name)) != OXM_OK) return st;
+    if ((st = check_view_memory(b, "rhs", name)) != OXM_OK) return st;
+    if ((st = check_view_memory(out, "out", name)) != OXM_OK) return st;
+    // operand strides over the output dims: right-aligned, 0 where broadcast
+    int64_t so[OXM_MAX_DIMS], sa[OXM_MAX_DIMS], sb[OXM_MAX_DIMS];
+    int64_t acc = 1;
+    for (int d = nd - 1; d >= 0; --d) {
+        so[d] = acc;
+        acc *= shape[d];
+        const int da = d - (nd - a->ndim), db = d - (nd - b->ndim);
+        sa[d] = (da >= 0 && a->shape[da] != 1) ? a->strides[da] : 0;
+        sb[d] = (db >= 0 && b->shape[db] != 1) ? b->strides[db] : 0;
+    }
+    const int64_t *sts[3] = {so, sa, sb};
+    oxm::EwShape sh = collapse(nd, shape, sts, 3);
+    const int es = dtype_size(a->dtype);
+    void *po = (char *)out->data + out->offset * es;
+    const void *pa = (const char *)a->data + a->offset * es, *pb = (const char *)b->data + b->offset * es;
+    const void *ptrs[3] = {po, pa, pb};
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = oxm::launch_elementwise(a->dtype, 2, op, sh, po, pa, pb, ew_vec(sh, 3, ptrs, es), s);
+    if (e != hipSuccess) return hip_fail(e, name);
+    return finish(s, name);
+}
+
+oxm_status oxm_reduce_infer(const oxm_view *x, const int32_t *axes, int32_t naxes, int32_t *out_ndim,
+                            int64_t *out_shape) {
+    const char *op = "reduce";
+    oxm_status st;
+    if ((st = check_view(x, "input", op)) != OXM_OK) return st;
+    if (!out_ndim || !out_shape || (naxes > 0 && !axes))
+        return fail(OXM_E_INVALID_ARGUMENT, "reduce: NULL axes or output pointer");
+    if (naxes < 0) return fail(OXM_E_INVALID_ARGUMENT, "reduce: negative axis count");
+    bool red[OXM_MAX_DIMS] = {};
+    for (int i = 0; i < naxes; ++i) {
+        if (axes[i] < 0 || axes[i] >= x->ndim)
+            return fail(OXM_E_INDEX_OUT_OF_BOUNDS, "index out of bounds: axis %d of a rank-%d tensor in reduce", axes[i],
+                        x->ndim);
+        if (red[axes[i]]) return fail(OXM_E_INVALID_ARGUMENT, "reduce: axis %d listed twice", axes[i]);
+        red[axes[i]] = true;
+    }
+    int n = 0;
+    for (int d = 0; d < x->ndim; ++d)
+        if (naxes > 0 && !red[d]) out_shape[n++] = x->shape[d];
+    *out_ndim = n;
+    return ok();
+}
+
+oxm_status oxm_reduce(int32_t op, const oxm_view *x, const int32_t *axes, int32_t naxes, const oxm_view *out,
+                      void *stream) {
+    if (op != OXM_RED_SUM && op != OXM_RED_MAX) return fail(OXM_E_INVALID_ARGUMENT, "reduce: unknown op %d", op);
+    const char *name = op == OXM_RED_SUM ? "sum" : "max";
+    oxm_status st;
+    int32_t nd = 0;
+    int64_t oshape[OXM_MAX_DIMS];
+    if ((st = oxm_reduce_infer(x, axes, naxes, &nd, oshape)) != OXM_OK) return st;
+    if ((st = check_view(out, "out", name)) != OXM_OK) return st;
+    if (!is_float_dtype(x->dtype))
+        return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by %s", dtype_name(x->dtype), name);
+    if (x->device < 0) return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s is not a HIP device in %s",
+                                   device_str(x->device).c_str(), name);
+    if ((st = check_out(out, x->dtype, nd, oshape, x->device, name)) != OXM_OK) return st;
+    bool red[OXM_MAX_DIMS] = {};
+    for (int i = 0; i < naxes; ++i) red[axes[i]] = true;
+    if (naxes == 0)
+        for (int d = 0; d < x->ndim; ++d) red[d] = true;
+    int64_t n_out = 1, n_red = 1;
+    for (int d = 0; d < x->ndim; ++d) (red[d] ? n_red : n_out) *= x->shape[d];
+    if (n_out == 0) return ok();
+    if (n_red == 0 && op == OXM_RED_MAX)
+        return fail(OXM_E_SHAPE_MISMATCH, "shape mismatch: max over an empty extent of %s has no identity",
+                    shape_str(x->ndim, x->shape).c_str());
+    DeviceGuard guard(x->device);
+    if ((st = check_view_memory(x, "input", name)) != OXM_OK) return st;
+    if ((st = check_view_memory(out, "out", name)) != OXM_OK) return st;
+    // kept and reduced dims, each collapsed where the input walks them as one
+    int64_t ks[OXM_MAX_DIMS], kt[OXM_MAX_DIMS], rs[OXM_MAX_DIMS], rt[OXM_MAX_DIMS];
+    int nk = 0, nr = 0;
+    for (int d = 0; d < x->ndim; ++d) {
+        if (red[d]) {
+            rs[nr] = x->shape[d];
+            rt[nr++] = x->strides[d];
+        } else {
+            ks[nk] = x->shape[d];
+            kt[nk++] = x->strides[d];
+        }
+    }
+    auto pack = [](int n, const int64_t *shape, const int64_t *stv, int64_t *oshape_, int64_t *ost) {
+        const int64_t *sts[3] = {stv, nullptr, nullptr};
+        oxm::EwShape c = collapse(n, shape, sts, 1);
+        for (int d = 0; d < c.ndim; ++d) {
+            oshape_[d] = c.shape[d];
+            ost[d] = c.st[0][d];
+        }
+        return c.ndim;
+    };
+    oxm::RedGeom g{};
+    g.n_out = n_out;
+    g.n_red = n_red;
+    g.nk = pack(nk, ks, kt, g.kshape, g.kst);
+    g.nr = pack(nr, rs, rt, g.rshape, g.rst);
+    if (n_red == 0) {  // sum over nothing: zeros
+        g.nr = 1;
+        g.rshape[0] = 0;
+        g.rst[0] = 0;
+    }
+    const int es = dtype_size(x->dtype);
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = oxm::launch_reduce(x->dtype, op, g, (const char *)x->data + x->offset * es,
+                                      (char *)out->data + out->offset * es, s);
+    if (e != hipSuccess) return hip_fail(e, name);
+    return finish(s, name);
+}
+
+oxm_status oxm_copy_view(const oxm_view *src, const oxm_view *dst, void *stream) {
+    const char *op = "contiguous";
+    oxm_status st;
+    if ((st = check_view(src, "src", op)) != OXM_OK) return st;
+    if ((st = check_view(dst, "dst", op)) != OXM_OK) return st;
+    if (dst->dtype != src->dtype)
+        return fail(OXM_E_DTYPE_MISMATCH, "dtype mismatch: expected %s, got %s in %s", dtype_name(src->dtype),
+                    dtype_name(dst->dtype), op);
+    if (dst->ndim != src->ndim || (src->ndim && memcmp(dst->shape, src->shape, 8 * src->ndim)))
+        return fail(OXM_E_SHAPE_MISMATCH, "shape mismatch: expected %s, got %s in %s",
+                    shape_str(src->ndim, src->shape).c_str(), shape_str(dst->ndim, dst->shape).c_str(), op);
+    if (src->device < 0 || dst->device != src->device)
+        return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s vs %s in %s", device_str(src->device).c_str(),
+                    device_str(dst->device).c_str(), op);
+    for (int d = 0; d < dst->ndim; ++d)
+        if (dst->shape[d] > 1 && dst->strides[d] == 0)
+            return fail(OXM_E_INVALID_ARGUMENT, "%s: the destination view repeats elements (stride 0)", op);
+    if (numel(src) == 0) return ok();
+    DeviceGuard guard(src->device);
+    if ((st = check_view_memory(src, "src", op)) != OXM_OK) return st;
+    if ((st = check_view_memory(dst, "dst", op)) != OXM_OK) return st;
+    const int64_t *sts[3] = {dst->strides, src->strides, nullptr};
+    oxm::EwShape sh = collapse(src->ndim, src->shape, sts, 2);
+    const int es = dtype_size(src->dtype);
+    void *pd = (char *)dst->data + dst->offset * es;
+    const void *ps = (const char *)src->data + src->offset * es;
+    const void *ptrs[3] = {pd, ps, nullptr};
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = oxm::launch_copy(es, sh, pd, ps, contig16(sh, 2, ptrs, es), s);
+    if (e != hipSuccess) return hip_fail(e, op);
+    return finish(s, op);
 }
 
 oxm_status oxm_synchronize(int32_t device) {

@@ -324,6 +324,42 @@ class Tensor:
         from .backend import backend_for
         return backend_for(self.device).sum(self, axes)
 
+    def max(self, axes: Sequence[int]) -> "Tensor":
+        from .backend import backend_for
+        return backend_for(self.device).max(self, axes)
+
+    def _be(self):
+        from .backend import backend_for
+        return backend_for(self.device)
+
+    def neg(self) -> "Tensor":
+        return self._be().neg(self)
+
+    def exp(self) -> "Tensor":
+        return self._be().exp(self)
+
+    def ln(self) -> "Tensor":
+        return self._be().ln(self)
+
+    def abs(self) -> "Tensor":
+        return self._be().abs(self)
+
+    def add(self, rhs: "Tensor") -> "Tensor":
+        return self._be().add(self, rhs)
+
+    def sub(self, rhs: "Tensor") -> "Tensor":
+        return self._be().sub(self, rhs)
+
+    def mul(self, rhs: "Tensor") -> "Tensor":
+        return self._be().mul(self, rhs)
+
+    def div(self, rhs: "Tensor") -> "Tensor":
+        return self._be().div(self, rhs)
+
+    def contiguous(self) -> "Tensor":
+        """tensor.rs:86-90: fresh contiguous storage; self when already contiguous."""
+        return self._be().contiguous(self)
+
     def __repr__(self) -> str:
         return f"Tensor(shape={list(self.shape)}, strides={list(self._layout.strides)}, " \
                f"offset={self._layout.offset}, dtype={self.dtype.name}, device={self.device})"
