@@ -268,6 +268,14 @@ def time_ops(steps: int = 20) -> dict:
     cases["mul bf16 [8192,8192] * [8192,1] (broadcast column)"] = (lambda: be.mul(hb, col, stream=s),
                                                                   2 * n * n * 2 + n * 2)
     cases["sum bf16 [8192,8192] over axis 1"] = (lambda: be.sum(hb, [1], stream=s), n * n * 2 + n * 2)
+    # SGD with momentum on a bf16 [4096, 16384] weight with its f32 gradient:
+    # reads p, g, v and writes p, v
+    pw = ox.Tensor.from_numpy(ox.f32_to_bf16_bits(rng.standard_normal((4096, 16384), dtype=np.float32)), dev,
+                              ox.DType.BF16)
+    gw = ox.Tensor.from_numpy(rng.standard_normal((4096, 16384), dtype=np.float32) * 1e-3, dev)
+    vw = ox.Tensor.from_numpy(np.zeros((4096, 16384), np.float32), dev)
+    cases["sgd momentum, bf16 param [4096,16384], f32 grad"] = (
+        lambda: be.sgd_step(pw, gw, vw, 1e-3, 0.9, 0.0, False, stream=s), 4096 * 16384 * (2 + 4 + 4 + 2 + 4))
     out = {}
     with torch.cuda.stream(ts):
         for name, (fn, nbytes) in cases.items():

@@ -162,14 +162,33 @@ oxm_status oxm_mse_loss_grad(const oxm_view *y, const oxm_view *t, const oxm_vie
  * view of x's shape and dtype ("a fresh contiguous tensor", :16-17).  exp
  * and ln follow the device's IEEE-754 float functions (ln of a negative is
  * NaN, of zero -inf). */
-typedef enum { OXM_UN_NEG = 0, OXM_UN_EXP = 1, OXM_UN_LN = 2, OXM_UN_ABS = 3 } oxm_unary_op;
+typedef enum {
+    OXM_UN_NEG = 0,
+    OXM_UN_EXP = 1,
+    OXM_UN_LN = 2,
+    OXM_UN_ABS = 3,
+    /* sign(x) in {-1, 0, +1}, NaN for NaN: no counterpart among the
+     * reference's UnaryOps; the derivative of abs for the autograd tape. */
+    OXM_UN_SIGN = 4
+} oxm_unary_op;
 oxm_status oxm_unary(int32_t op, const oxm_view *x, const oxm_view *out, void *stream);
 
 /* BinaryOps (crates/oxmera-ops/src/lib.rs:39-50): out = a op b with NumPy
  * broadcasting (crates/oxmera-core/src/shape.rs:45-58; BroadcastIncompatible
  * otherwise).  a, b: same dtype (F32/F64/BF16/F16) and device, any strides;
  * out: contiguous, the broadcast shape.  Float division follows IEEE-754. */
-typedef enum { OXM_BIN_ADD = 0, OXM_BIN_SUB = 1, OXM_BIN_MUL = 2, OXM_BIN_DIV = 3 } oxm_binary_op;
+typedef enum {
+    OXM_BIN_ADD = 0,
+    OXM_BIN_SUB = 1,
+    OXM_BIN_MUL = 2,
+    OXM_BIN_DIV = 3,
+    /* The two below have no counterpart among the reference's BinaryOps;
+     * the autograd tape uses them.  EQ: 1 where a == b, else 0 (the mask of
+     * max's gradient).  DGELU: a * GELU'(b) with the erf GELU, the
+     * gradient through a GELU whose pre-activation is b. */
+    OXM_BIN_EQ = 4,
+    OXM_BIN_DGELU = 5
+} oxm_binary_op;
 oxm_status oxm_binary(int32_t op, const oxm_view *a, const oxm_view *b, const oxm_view *out, void *stream);
 
 /* ReduceOps (crates/oxmera-ops/src/lib.rs:61-69): sum or max over `axes`,
@@ -190,6 +209,28 @@ oxm_status oxm_reduce(int32_t op, const oxm_view *x, const int32_t *axes, int32_
  * HIP device; src any strides, dst any strides that do not repeat elements
  * (a contiguous dst gives contiguous()). */
 oxm_status oxm_copy_view(const oxm_view *src, const oxm_view *dst, void *stream);
+
+/* dst = src converted element by element between float dtypes (F32, F64,
+ * BF16, F16): widened exactly, rounded once to nearest-even (F64 -> 16-bit
+ * rounds through f32).  Same shape and HIP device; src any strides, dst any
+ * strides that do not repeat elements.  No counterpart in the reference
+ * (it has no dtype conversion yet); the autograd tape uses it where a
+ * gradient's dtype differs from its operand's (an f32 GEMM result flowing
+ * back into a 16-bit operand). */
+oxm_status oxm_convert(const oxm_view *src, const oxm_view *dst, void *stream);
+
+/* One SGD step over one parameter, in place, fused (the reserved
+ * crates/oxmera-optim/src/lib.rs:1-11 defines no optimizer yet; semantics
+ * as torch.optim.SGD with dampening 0), per element in f32 with each
+ * operation rounded separately (no fused multiply-add):
+ *   g = grad (+ weight_decay * p)
+ *   momentum != 0:  v = momentum * v + g;  g = nesterov ? g + momentum * v : v
+ *   p = p - lr * g, rounded once to p's dtype.
+ * param: contiguous F32, BF16 or F16; grad: contiguous, same shape, F32 or
+ * param's dtype; velocity: NULL when momentum == 0, else a contiguous F32
+ * buffer of the same shape (zeros before the first step). */
+oxm_status oxm_sgd_step(const oxm_view *param, const oxm_view *grad, const oxm_view *velocity, float lr,
+                        float momentum, float weight_decay, int32_t nesterov, void *stream);
 
 /* Storage for device tensors (crates/oxmera-tensor/src/storage.rs:12-32,
  * "GPU variants hold opaque backend handles", :19-24). */

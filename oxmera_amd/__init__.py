@@ -2,11 +2,12 @@
 
 Layers:
   ``liboxm.so``   C-ABI (include/oxm.h): HIP MFMA GEMM kernels for strided
-                  views, fused bias/GELU epilogues, bias-gradient and MSE kernels.
+                  views, fused bias/GELU epilogues, bias-gradient and MSE kernels,
+                  elementwise / reduction / copy kernels, the fused SGD update.
   ``core``        oxmera-core vocabulary (DType, Layout, Device, typed errors).
   ``tensor``      Storage / Tensor views (never copied on the GEMM path).
-  ``backend``     HipBackend (MatmulOps, ReduceOps) and the device registry.
-  ``autograd``/``nn``  the tape and Linear layers of the MLP training step.
+  ``backend``     HipBackend (Matmul, Unary, Binary, Reduce ops) and the device registry.
+  ``autograd``/``nn``/``optim``  the tape, Linear layers and SGD.
 """
 from . import _lib
 from .core import (BackendUnavailable, BroadcastIncompatible, Device, DeviceMismatch, DType, DTypeMismatch,

@@ -33,8 +33,8 @@ ACT_NONE = 0
 ACT_GELU = 1
 ACT_DGELU = 2
 
-UN_NEG, UN_EXP, UN_LN, UN_ABS = 0, 1, 2, 3
-BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV = 0, 1, 2, 3
+UN_NEG, UN_EXP, UN_LN, UN_ABS, UN_SIGN = 0, 1, 2, 3, 4
+BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV, BIN_EQ, BIN_DGELU = 0, 1, 2, 3, 4, 5
 RED_SUM, RED_MAX = 0, 1
 
 
@@ -82,6 +82,9 @@ _PROTOS = {
     "oxm_reduce": (C.c_int, [C.c_int32, C.POINTER(OxmView), C.POINTER(C.c_int32), C.c_int32, C.POINTER(OxmView),
                              C.c_void_p]),
     "oxm_copy_view": (C.c_int, [C.POINTER(OxmView), C.POINTER(OxmView), C.c_void_p]),
+    "oxm_convert": (C.c_int, [C.POINTER(OxmView), C.POINTER(OxmView), C.c_void_p]),
+    "oxm_sgd_step": (C.c_int, [C.POINTER(OxmView), C.POINTER(OxmView), C.POINTER(OxmView), C.c_float, C.c_float,
+                               C.c_float, C.c_int32, C.c_void_p]),
     "oxm_alloc": (C.c_int, [C.c_int32, C.c_size_t, C.POINTER(C.c_void_p)]),
     "oxm_free": (C.c_int, [C.c_int32, C.c_void_p]),
     "oxm_copy": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_size_t, C.c_void_p]),

@@ -137,6 +137,37 @@ class HipBackend:
 
     def div(self, lhs, rhs, *, stream=None): return self._binary(_lib.BIN_DIV, lhs, rhs, stream)
 
+    # ---- what the autograd tape adds (no counterpart among the reference's ops) ----
+    def sign(self, a, *, stream=None):
+        """-1, 0 or +1 per element (NaN stays NaN): abs's derivative."""
+        return self._unary(_lib.UN_SIGN, a, stream)
+
+    def eq(self, lhs, rhs, *, stream=None):
+        """1 where lhs == rhs else 0, broadcasting: max's gradient mask."""
+        return self._binary(_lib.BIN_EQ, lhs, rhs, stream)
+
+    def dgelu(self, grad, z, *, stream=None):
+        """grad * GELU'(z) (erf GELU): the gradient through a GELU."""
+        return self._binary(_lib.BIN_DGELU, grad, z, stream)
+
+    def convert(self, a: Tensor, dtype: DType, *, stream: int | None = None) -> Tensor:
+        """a in ``dtype`` (fresh contiguous storage), rounded once to nearest
+        even; a itself when it already has that dtype."""
+        if a.dtype == dtype:
+            return a
+        out = Tensor.empty(a.shape, dtype, a.device)
+        x, o = a.abi_view(), out.abi_view()
+        check(_lib.lib().oxm_convert(C.byref(x), C.byref(o), self._s(stream)))
+        return out
+
+    def sgd_step(self, param: Tensor, grad: Tensor, velocity: Tensor | None, lr: float, momentum: float = 0.0,
+                 weight_decay: float = 0.0, nesterov: bool = False, *, stream: int | None = None) -> None:
+        """One fused SGD update of ``param`` in place (oxm_sgd_step)."""
+        p, g = param.abi_view(), grad.abi_view()
+        v = velocity.abi_view() if velocity is not None else None
+        check(_lib.lib().oxm_sgd_step(C.byref(p), C.byref(g), C.byref(v) if v is not None else None, float(lr),
+                                      float(momentum), float(weight_decay), int(bool(nesterov)), self._s(stream)))
+
     # ---- Tensor::contiguous ----
     def contiguous(self, a: Tensor, *, stream: int | None = None) -> Tensor:
         """a's elements in logical order in fresh contiguous storage; a itself

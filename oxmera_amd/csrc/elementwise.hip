@@ -65,8 +65,20 @@ __device__ __forceinline__ A apply_unary(A x) {
         return exp(x);
     else if constexpr (OP == kUnLn)
         return log(x);
-    else
+    else if constexpr (OP == kUnAbs)
         return fabs(x);
+    else  // sign; NaN stays NaN
+        return x > A(0) ? A(1) : (x < A(0) ? A(-1) : x * A(0));
+}
+
+// GELU'(x) for the erf GELU: Phi(x) + x phi(x).
+template <typename A>
+__device__ __forceinline__ A dgelu_acc(A x) {
+    if constexpr (std::is_same<A, float>::value) {
+        return dgelu_erf(x);
+    } else {
+        return 0.5 * (1.0 + erf(x * 0.70710678118654752440)) + x * 0.39894228040143267794 * exp(-0.5 * x * x);
+    }
 }
 
 template <int OP, typename A>
@@ -77,8 +89,12 @@ __device__ __forceinline__ A apply_binary(A a, A b) {
         return a - b;
     else if constexpr (OP == kBinMul)
         return a * b;
-    else
+    else if constexpr (OP == kBinDiv)
         return a / b;
+    else if constexpr (OP == kBinEq)
+        return a == b ? A(1) : A(0);
+    else
+        return a * dgelu_acc<A>(b);
 }
 
 // Offsets of element `i` (row-major over `shape`) in up to three strided
@@ -287,6 +303,55 @@ __global__ void __launch_bounds__(256) copy_transpose(EwShape s, int p, U *dst, 
     for (int k = 0; k < kTT / 4; ++k) {
         const int i = ty + 4 * k;
         if (p0 + i < np_ && l0 + tx < nl) dst[od + (p0 + i) * dp + (l0 + tx)] = tile[tx][i];
+    }
+}
+
+// ---- dtype conversion --------------------------------------------------------------
+
+template <int DI, int DO>
+__global__ void __launch_bounds__(256) convert_strided(EwShape s, void *dst, const void *src) {
+    const int64_t inner = s.shape[s.ndim - 1];
+    const int64_t runs_per_row = (inner + kRun - 1) / kRun;
+    const int64_t nruns = s.numel / inner * runs_per_row;
+    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < nruns; r += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = r / runs_per_row, c0 = (r - row * runs_per_row) * kRun;
+        int64_t od, os, unused;
+        Coord::offsets(s, row * inner + c0, od, os, unused);
+        const int64_t sd = s.st[0][s.ndim - 1], ss = s.st[1][s.ndim - 1];
+#pragma unroll
+        for (int k = 0; k < kRun; ++k) {
+            if (c0 + k >= inner) break;
+            El<DO>::store(dst, od + k * sd, (typename El<DO>::Acc)El<DI>::load(src, os + k * ss));
+        }
+    }
+}
+
+// ---- SGD ---------------------------------------------------------------------------
+
+// A product the compiler may not fuse into a following add: the empty asm
+// takes the value through a VGPR, so the multiply is rounded on its own.
+__device__ __forceinline__ float unfused_mul(float a, float b) {
+    float m = a * b;
+    asm volatile("" : "+v"(m));
+    return m;
+}
+
+// MODE 0: plain, 1: momentum, 2: Nesterov momentum.  Each f32 operation is
+// rounded on its own (no fused multiply-adds), so the result is reproducible
+// operation by operation.
+template <int PDT, int GDT, int MODE, bool WD>
+__global__ void __launch_bounds__(256) sgd_kernel(int64_t n, void *p, const void *g, float *v, float lr, float mu,
+                                                  float wd) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float pv = El<PDT>::load(p, i);
+        float gv = El<GDT>::load(g, i);
+        if constexpr (WD) gv = gv + unfused_mul(wd, pv);
+        if constexpr (MODE != 0) {
+            const float vv = unfused_mul(mu, v[i]) + gv;
+            v[i] = vv;
+            gv = MODE == 2 ? gv + unfused_mul(mu, vv) : vv;
+        }
+        El<PDT>::store(p, i, pv - unfused_mul(lr, gv));
     }
 }
 
@@ -517,14 +582,17 @@ hipError_t ew_dispatch(int nops, int op, const EwShape &s, void *out, const void
         case kUnNeg: return ew_launch<DT, 1, kUnNeg>(s, out, x, y, vec, st);
         case kUnExp: return ew_launch<DT, 1, kUnExp>(s, out, x, y, vec, st);
         case kUnLn: return ew_launch<DT, 1, kUnLn>(s, out, x, y, vec, st);
-        default: return ew_launch<DT, 1, kUnAbs>(s, out, x, y, vec, st);
+        case kUnAbs: return ew_launch<DT, 1, kUnAbs>(s, out, x, y, vec, st);
+        default: return ew_launch<DT, 1, kUnSign>(s, out, x, y, vec, st);
         }
     }
     switch (op) {
     case kBinAdd: return ew_launch<DT, 2, kBinAdd>(s, out, x, y, vec, st);
     case kBinSub: return ew_launch<DT, 2, kBinSub>(s, out, x, y, vec, st);
     case kBinMul: return ew_launch<DT, 2, kBinMul>(s, out, x, y, vec, st);
-    default: return ew_launch<DT, 2, kBinDiv>(s, out, x, y, vec, st);
+    case kBinDiv: return ew_launch<DT, 2, kBinDiv>(s, out, x, y, vec, st);
+    case kBinEq: return ew_launch<DT, 2, kBinEq>(s, out, x, y, vec, st);
+    default: return ew_launch<DT, 2, kBinDGelu>(s, out, x, y, vec, st);
     }
 }
 
@@ -641,6 +709,60 @@ hipError_t launch_copy(int elem_bytes, const EwShape &s, void *dst, const void *
     default: hipLaunchKernelGGL(copy_strided<uint64_t>, grid, dim3(256), 0, st, s, (uint64_t *)dst, (const uint64_t *)src); break;
     }
     return hipGetLastError();
+}
+
+namespace {
+template <int DI>
+hipError_t convert_from(int dto, const EwShape &s, void *dst, const void *src, hipStream_t st) {
+    const int64_t runs = s.numel / s.shape[s.ndim - 1] * ((s.shape[s.ndim - 1] + kRun - 1) / kRun);
+    const dim3 grid(grid_for(runs));
+    switch (dto) {
+    case kDtF32: hipLaunchKernelGGL((convert_strided<DI, kDtF32>), grid, dim3(256), 0, st, s, dst, src); break;
+    case kDtBF16: hipLaunchKernelGGL((convert_strided<DI, kDtBF16>), grid, dim3(256), 0, st, s, dst, src); break;
+    case kDtF16: hipLaunchKernelGGL((convert_strided<DI, kDtF16>), grid, dim3(256), 0, st, s, dst, src); break;
+    default: hipLaunchKernelGGL((convert_strided<DI, kDtF64>), grid, dim3(256), 0, st, s, dst, src); break;
+    }
+    return hipGetLastError();
+}
+
+template <int PDT, int GDT>
+hipError_t sgd_typed(int64_t n, void *p, const void *g, float *v, float lr, float mu, float wd, bool nesterov,
+                     hipStream_t st) {
+    const dim3 grid(grid_for(n)), block(256);
+    const bool w = wd != 0.0f;
+    if (mu == 0.0f) {
+        if (w) hipLaunchKernelGGL((sgd_kernel<PDT, GDT, 0, true>), grid, block, 0, st, n, p, g, v, lr, mu, wd);
+        else hipLaunchKernelGGL((sgd_kernel<PDT, GDT, 0, false>), grid, block, 0, st, n, p, g, v, lr, mu, wd);
+    } else if (!nesterov) {
+        if (w) hipLaunchKernelGGL((sgd_kernel<PDT, GDT, 1, true>), grid, block, 0, st, n, p, g, v, lr, mu, wd);
+        else hipLaunchKernelGGL((sgd_kernel<PDT, GDT, 1, false>), grid, block, 0, st, n, p, g, v, lr, mu, wd);
+    } else {
+        if (w) hipLaunchKernelGGL((sgd_kernel<PDT, GDT, 2, true>), grid, block, 0, st, n, p, g, v, lr, mu, wd);
+        else hipLaunchKernelGGL((sgd_kernel<PDT, GDT, 2, false>), grid, block, 0, st, n, p, g, v, lr, mu, wd);
+    }
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_convert(int dti, int dto, const EwShape &s, void *dst, const void *src, hipStream_t st) {
+    if (s.numel == 0) return hipSuccess;
+    switch (dti) {
+    case kDtF32: return convert_from<kDtF32>(dto, s, dst, src, st);
+    case kDtBF16: return convert_from<kDtBF16>(dto, s, dst, src, st);
+    case kDtF16: return convert_from<kDtF16>(dto, s, dst, src, st);
+    default: return convert_from<kDtF64>(dto, s, dst, src, st);
+    }
+}
+
+hipError_t launch_sgd(int pdt, int gdt, int64_t n, void *p, const void *g, float *v, float lr, float momentum,
+                      float weight_decay, bool nesterov, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    if (pdt == kDtF32) return sgd_typed<kDtF32, kDtF32>(n, p, g, v, lr, momentum, weight_decay, nesterov, st);
+    if (pdt == kDtBF16)
+        return gdt == kDtF32 ? sgd_typed<kDtBF16, kDtF32>(n, p, g, v, lr, momentum, weight_decay, nesterov, st)
+                             : sgd_typed<kDtBF16, kDtBF16>(n, p, g, v, lr, momentum, weight_decay, nesterov, st);
+    return gdt == kDtF32 ? sgd_typed<kDtF16, kDtF32>(n, p, g, v, lr, momentum, weight_decay, nesterov, st)
+                         : sgd_typed<kDtF16, kDtF16>(n, p, g, v, lr, momentum, weight_decay, nesterov, st);
 }
 
 hipError_t launch_reduce(int dtype, int op, const RedGeom &g, const void *x, void *out, hipStream_t st) {

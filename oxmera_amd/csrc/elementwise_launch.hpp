@@ -7,8 +7,8 @@ namespace oxm {
 
 constexpr int kDtF64 = 1;  // oxm_dtype F64 (F32 = 0, BF16 = 6, F16 = 7 are in gemm_kernels.hpp)
 
-enum UnaryOp : int { kUnNeg = 0, kUnExp = 1, kUnLn = 2, kUnAbs = 3 };
-enum BinaryOp : int { kBinAdd = 0, kBinSub = 1, kBinMul = 2, kBinDiv = 3 };
+enum UnaryOp : int { kUnNeg = 0, kUnExp = 1, kUnLn = 2, kUnAbs = 3, kUnSign = 4 };
+enum BinaryOp : int { kBinAdd = 0, kBinSub = 1, kBinMul = 2, kBinDiv = 3, kBinEq = 4, kBinDGelu = 5 };
 enum ReduceOp : int { kRedSum = 0, kRedMax = 1 };
 
 constexpr int kEwMaxDims = 8;
@@ -48,5 +48,14 @@ hipError_t launch_elementwise(int dtype, int nops, int op, const EwShape &s, voi
 hipError_t launch_copy(int elem_bytes, const EwShape &s, void *dst, const void *src, bool contig16, hipStream_t st);
 
 hipError_t launch_reduce(int dtype, int op, const RedGeom &g, const void *x, void *out, hipStream_t st);
+
+// dst = src converted from dtype dti to dtype dto (float dtypes); operand 0
+// of s is dst, operand 1 src.
+hipError_t launch_convert(int dti, int dto, const EwShape &s, void *dst, const void *src, hipStream_t st);
+
+// One fused SGD step over n contiguous elements (see oxm_sgd_step); v is
+// null when momentum == 0.
+hipError_t launch_sgd(int pdt, int gdt, int64_t n, void *p, const void *g, float *v, float lr, float momentum,
+                      float weight_decay, bool nesterov, hipStream_t st);
 
 }  // namespace oxm

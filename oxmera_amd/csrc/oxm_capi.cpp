@@ -6,6 +6,7 @@
 // pick a global loader; fill the kernel argument block and launch.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -341,12 +342,12 @@ int ew_vec(const oxm::EwShape &s, int nops, const void *const ptr[3], int es) {
 }
 
 const char *unary_name(int op) {
-    static const char *n[] = {"neg", "exp", "ln", "abs"};
-    return op >= 0 && op < 4 ? n[op] : "unary";
+    static const char *n[] = {"neg", "exp", "ln", "abs", "sign"};
+    return op >= 0 && op < 5 ? n[op] : "unary";
 }
 const char *binary_name(int op) {
-    static const char *n[] = {"add", "sub", "mul", "div"};
-    return op >= 0 && op < 4 ? n[op] : "binary";
+    static const char *n[] = {"add", "sub", "mul", "div", "eq", "dgelu"};
+    return op >= 0 && op < 6 ? n[op] : "binary";
 }
 
 // The checks every elementwise output needs: dtype, shape, contiguity,
@@ -700,7 +701,7 @@ oxm_status oxm_copy(void *dst, int32_t dst_device, const void *src, int32_t src_
 }
 
 oxm_status oxm_unary(int32_t op, const oxm_view *x, const oxm_view *out, void *stream) {
-    if (op < OXM_UN_NEG || op > OXM_UN_ABS) return fail(OXM_E_INVALID_ARGUMENT, "unary: unknown op %d", op);
+    if (op < OXM_UN_NEG || op > OXM_UN_SIGN) return fail(OXM_E_INVALID_ARGUMENT, "unary: unknown op %d", op);
     const char *name = unary_name(op);
     oxm_status st;
     if ((st = check_view(x, "input", name)) != OXM_OK) return st;
@@ -733,7 +734,7 @@ oxm_status oxm_unary(int32_t op, const oxm_view *x, const oxm_view *out, void *s
 }
 
 oxm_status oxm_binary(int32_t op, const oxm_view *a, const oxm_view *b, const oxm_view *out, void *stream) {
-    if (op < OXM_BIN_ADD || op > OXM_BIN_DIV) return fail(OXM_E_INVALID_ARGUMENT, "binary: unknown op %d", op);
+    if (op < OXM_BIN_ADD || op > OXM_BIN_DGELU) return fail(OXM_E_INVALID_ARGUMENT, "binary: unknown op %d", op);
     const char *name = binary_name(op);
     oxm_status st;
     if ((st = check_view(a, "lhs", name)) != OXM_OK) return st;
@@ -900,6 +901,88 @@ oxm_status oxm_copy_view(const oxm_view *src, const oxm_view *dst, void *stream)
     const void *ptrs[3] = {pd, ps, nullptr};
     hipStream_t s = (hipStream_t)stream;
     hipError_t e = oxm::launch_copy(es, sh, pd, ps, contig16(sh, 2, ptrs, es), s);
+    if (e != hipSuccess) return hip_fail(e, op);
+    return finish(s, op);
+}
+
+oxm_status oxm_convert(const oxm_view *src, const oxm_view *dst, void *stream) {
+    const char *op = "convert";
+    oxm_status st;
+    if ((st = check_view(src, "src", op)) != OXM_OK) return st;
+    if ((st = check_view(dst, "dst", op)) != OXM_OK) return st;
+    if (!is_float_dtype(src->dtype))
+        return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by %s", dtype_name(src->dtype), op);
+    if (!is_float_dtype(dst->dtype))
+        return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by %s", dtype_name(dst->dtype), op);
+    if (dst->ndim != src->ndim || (src->ndim && memcmp(dst->shape, src->shape, 8 * src->ndim)))
+        return fail(OXM_E_SHAPE_MISMATCH, "shape mismatch: expected %s, got %s in %s",
+                    shape_str(src->ndim, src->shape).c_str(), shape_str(dst->ndim, dst->shape).c_str(), op);
+    if (src->device < 0 || dst->device != src->device)
+        return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s vs %s in %s", device_str(src->device).c_str(),
+                    device_str(dst->device).c_str(), op);
+    for (int d = 0; d < dst->ndim; ++d)
+        if (dst->shape[d] > 1 && dst->strides[d] == 0)
+            return fail(OXM_E_INVALID_ARGUMENT, "%s: the destination view repeats elements (stride 0)", op);
+    if (numel(src) == 0) return ok();
+    DeviceGuard guard(src->device);
+    if ((st = check_view_memory(src, "src", op)) != OXM_OK) return st;
+    if ((st = check_view_memory(dst, "dst", op)) != OXM_OK) return st;
+    const int64_t *sts[3] = {dst->strides, src->strides, nullptr};
+    oxm::EwShape sh = collapse(src->ndim, src->shape, sts, 2);
+    void *pd = (char *)dst->data + dst->offset * dtype_size(dst->dtype);
+    const void *ps = (const char *)src->data + src->offset * dtype_size(src->dtype);
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = oxm::launch_convert(src->dtype, dst->dtype, sh, pd, ps, s);
+    if (e != hipSuccess) return hip_fail(e, op);
+    return finish(s, op);
+}
+
+oxm_status oxm_sgd_step(const oxm_view *param, const oxm_view *grad, const oxm_view *velocity, float lr,
+                        float momentum, float weight_decay, int32_t nesterov, void *stream) {
+    const char *op = "sgd_step";
+    oxm_status st;
+    if ((st = check_view(param, "param", op)) != OXM_OK) return st;
+    if ((st = check_view(grad, "grad", op)) != OXM_OK) return st;
+    if (param->dtype != OXM_F32 && param->dtype != OXM_BF16 && param->dtype != OXM_F16)
+        return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by %s", dtype_name(param->dtype), op);
+    if (grad->dtype != OXM_F32 && grad->dtype != param->dtype)
+        return fail(OXM_E_DTYPE_MISMATCH, "dtype mismatch: expected %s or F32, got %s in %s (grad)",
+                    dtype_name(param->dtype), dtype_name(grad->dtype), op);
+    if (!std::isfinite(lr) || !std::isfinite(momentum) || !std::isfinite(weight_decay))
+        return fail(OXM_E_INVALID_ARGUMENT, "%s: lr, momentum and weight_decay must be finite", op);
+    if (nesterov && momentum == 0.0f)
+        return fail(OXM_E_INVALID_ARGUMENT, "%s: Nesterov momentum needs momentum != 0", op);
+    if ((momentum != 0.0f) != (velocity != nullptr))
+        return fail(OXM_E_INVALID_ARGUMENT, "%s: a velocity buffer is required exactly when momentum != 0", op);
+    if (velocity && (st = check_view(velocity, "velocity", op)) != OXM_OK) return st;
+    if (velocity && velocity->dtype != OXM_F32)
+        return fail(OXM_E_DTYPE_MISMATCH, "dtype mismatch: expected F32, got %s in %s (velocity)",
+                    dtype_name(velocity->dtype), op);
+    const oxm_view *vs[3] = {param, grad, velocity};
+    const char *names[3] = {"param", "grad", "velocity"};
+    for (int i = 0; i < 3; ++i) {
+        const oxm_view *v = vs[i];
+        if (!v) continue;
+        if (i > 0 && (v->ndim != param->ndim || (param->ndim && memcmp(v->shape, param->shape, 8 * param->ndim))))
+            return fail(OXM_E_SHAPE_MISMATCH, "shape mismatch: expected %s, got %s in %s (%s)",
+                        shape_str(param->ndim, param->shape).c_str(), shape_str(v->ndim, v->shape).c_str(), op,
+                        names[i]);
+        if (v->device < 0 || v->device != param->device)
+            return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s vs %s in %s (%s)",
+                        device_str(param->device).c_str(), device_str(v->device).c_str(), op, names[i]);
+        if (!is_contiguous(v))
+            return fail(OXM_E_NOT_IMPLEMENTED, "%s is not implemented for a non-contiguous %s", op, names[i]);
+    }
+    const int64_t n = numel(param);
+    if (n == 0) return ok();
+    DeviceGuard guard(param->device);
+    for (int i = 0; i < 3; ++i)
+        if (vs[i] && (st = check_view_memory(vs[i], names[i], op)) != OXM_OK) return st;
+    void *pp = (char *)param->data + param->offset * dtype_size(param->dtype);
+    const void *pg = (const char *)grad->data + grad->offset * dtype_size(grad->dtype);
+    float *pv = velocity ? (float *)velocity->data + velocity->offset : nullptr;
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = oxm::launch_sgd(param->dtype, grad->dtype, n, pp, pg, pv, lr, momentum, weight_decay, nesterov != 0, s);
     if (e != hipSuccess) return hip_fail(e, op);
     return finish(s, op);
 }

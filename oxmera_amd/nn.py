@@ -30,6 +30,9 @@ class Linear:
     def __call__(self, x: Var) -> Var:
         return linear(x, self.w, self.b, self.act)
 
+    def parameters(self) -> list:
+        return [self.w] + ([self.b] if self.b is not None else [])
+
     def zero_grad(self) -> None:
         self.w.grad = None
         if self.b is not None:
@@ -44,6 +47,9 @@ class MLP2:
 
     def __call__(self, x: Var) -> Var:
         return self.fc2(self.fc1(x))
+
+    def parameters(self) -> list:
+        return self.fc1.parameters() + self.fc2.parameters()
 
     def train_step(self, x: Var, target: Tensor) -> Var:
         """Forward, MSE against ``target`` and backward; returns the loss."""

@@ -176,7 +176,8 @@ class Tensor:
             host = arr if arr.dtype == np.uint16 else f32_to_bf16_bits(arr.astype(np.float32))
         else:
             host = arr.astype(_np_dtype(dtype))
-        host = np.ascontiguousarray(host)
+        if not host.flags.c_contiguous:
+            host = host.copy(order="C")  # (np.ascontiguousarray would turn a 0-d array into shape (1,))
         t = Tensor.empty(host.shape, dtype, device)
         t._storage_write(host)
         return t
@@ -195,7 +196,7 @@ class Tensor:
         if nbytes == 0:
             return
         if self.device.kind == "cpu":
-            self._storage._host[:nbytes] = host.view(np.uint8).reshape(-1)
+            self._storage._host[:nbytes] = host.reshape(-1).view(np.uint8)
         else:
             check(_lib.lib().oxm_copy(C.c_void_p(self._storage.ptr), self.device.index,
                                       C.c_void_p(host.ctypes.data), -1, nbytes, None))

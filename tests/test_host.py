@@ -261,3 +261,9 @@ def test_bf16_host_rounding_matches_oracle(oracle):
     rng = np.random.default_rng(1)
     x = rng.normal(size=10000).astype(np.float32)
     assert np.array_equal(ox.f32_to_bf16_bits(x), oracle.bf16_round(x))
+
+
+def test_from_numpy_keeps_rank_zero():
+    import oxmera_amd as ox
+    t = ox.Tensor.from_numpy(np.array(2.5, np.float32), ox.Device.cpu())
+    assert t.shape == () and t.to_numpy().shape == () and float(t.to_numpy()) == 2.5
