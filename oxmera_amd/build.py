@@ -47,6 +47,28 @@ def _compile(src: str) -> Path:
     return obj
 
 
+CLI_SRC = PKG / "cli" / "doctor.cpp"
+CLI = PKG / "bin" / "oxmera"
+
+
+def build_cli(verbose: bool = True) -> Path:
+    """Compile the ``oxmera`` command (``oxmera doctor``) with the host C++
+    compiler; returns its path."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no host C++ compiler: the oxmera command cannot be built")
+    CLI.parent.mkdir(exist_ok=True)
+    tmp = CLI.with_suffix(".tmp")
+    cmd = [cxx, "-O2", "-std=c++17", "-Wall", "-o", str(tmp), str(CLI_SRC)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, CLI)
+    if verbose:
+        print(f"built {CLI}", flush=True)
+    return CLI
+
+
 def build(verbose: bool = True) -> Path:
     """Compile every translation unit and link ``liboxm.so``; returns its path."""
     BUILD.mkdir(exist_ok=True)
@@ -66,4 +88,5 @@ def build(verbose: bool = True) -> Path:
 
 if __name__ == "__main__":
     build()
+    build_cli()
     sys.exit(0)
