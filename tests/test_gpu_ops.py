@@ -2,8 +2,9 @@
 Tensor::contiguous) against oracle/ops_ref.py, through the C-ABI.
 
 Bars: neg / abs / add / sub / mul / div and copies are bit-exact (one
-operation, one rounding, as the oracle); exp / ln within 4 f32 ulp before the
-final rounding (device float functions), i.e. <= 1 ulp of a 16-bit output;
+operation, one rounding, as the oracle); exp / ln within 4 ulp for f32 and
+f64 (device float functions against numpy's float64 ones), <= 1 ulp of a
+16-bit output;
 max bit-exact; sum within the f32 summation bound n * 2^-24 * sum |x| (plus
 one rounding of the output dtype).
 """
