@@ -31,6 +31,31 @@ hipError_t pick_dl(const GemmArgs &a, int la, int lb, hipStream_t s) {
     return launch_dl<T, BM, BN, WM, WN, NS, BKS, true, true>(a, s);
 }
 
+// The epilogue only stores C (no bias, activation or column sums).  The
+// one-wave-per-SIMD kernel is the faster one then (8192^3 NT f32 out: 0.80
+// vs 0.86 ms); with an epilogue that does work per element its 128 x 128
+// wave tiles leave the CU with too few waves to hide it (the MLP's forward
+// and dZ1 GEMMs: 1.27 vs 1.10 ms), and the 2x4-wave kernel is used.
+inline bool plain_epilogue(const GemmArgs &a) { return a.act == kActNone && !a.bias && !a.colsum; }
+
+// Direct-to-LDS kernel with one wave per SIMD (2x2 waves, hand-placed stream).
+template <typename T, bool AMN, bool BMN>
+hipError_t launch_dli(GemmArgs a, hipStream_t s) {
+    a.group_m = 4;
+    int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n * a.batch;
+    dim3 grid((unsigned)ntiles), block(256);
+    hipLaunchKernelGGL((gemm_kernel_dli<T, 256, 256, 64, AMN, BMN>), grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t pick_dli(const GemmArgs &a, int la, int lb, hipStream_t s) {
+    if (la == kLdK && lb == kLdK) return launch_dli<T, false, false>(a, s);
+    if (la == kLdK) return launch_dli<T, false, true>(a, s);
+    if (lb == kLdK) return launch_dli<T, true, false>(a, s);
+    return launch_dli<T, true, true>(a, s);
+}
+
 template <typename T, int BM, int BN, int WM, int WN, Ld LA>
 hipError_t pick_b(const GemmArgs &a, int lb, hipStream_t s) {
     switch (lb) {

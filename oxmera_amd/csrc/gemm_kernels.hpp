@@ -499,42 +499,41 @@ __device__ __forceinline__ float stored_value(float x) {
         return f16_bits_to_f32(f32_to_f16_bits(x));
 }
 
-// Applies the epilogue to 4 adjacent outputs (row-major offset o, column col,
-// nvalid of them inside N) and stores them; with p.colsum, adds the stored
-// values to cs.
+// Four consecutive elements of a C-shaped array (OUT_DT) at element offset o,
+// as f32.  `vec`: the four are in range and 16-byte aligned (one vector load);
+// otherwise the first nvalid are loaded one by one and the rest read as 0.
 template <int OUT_DT>
-__device__ __forceinline__ void store4(const GemmArgs &p, int64_t o, int64_t col, float4 v, bool vec, int nvalid,
-                                       float (&cs)[4]) {
-    float x[4] = {v.x, v.y, v.z, v.w};
-    if (p.act == kActDGelu) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (i < nvalid) x[i] *= dgelu_erf(load_out<OUT_DT>(p.aux, o + i));
-    } else {
-        if (p.bias) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (i < nvalid) x[i] += load_as_f32(p.bias, p.bias_dtype, col + i);
-        }
-        if (p.act == kActGelu) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (i < nvalid) {
-                    if (p.aux) store_out<OUT_DT>(p.aux, o + i, x[i]);
-                    x[i] = gelu_erf(x[i]);
-                }
-            }
-        }
-    }
-    if (p.colsum) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (i < nvalid) cs[i] += stored_value<OUT_DT>(x[i]);
-    }
+__device__ __forceinline__ void load4_out(const void *c, int64_t o, bool vec, int nvalid, float (&z)[4]) {
     if (vec) {
         if constexpr (OUT_DT == kDtF32) {
-            *(float4 *)((float *)p.c + o) = make_float4(x[0], x[1], x[2], x[3]);
+            const f32x4_t v = *(const f32x4_t *)((const float *)c + o);
+            z[0] = v[0], z[1] = v[1], z[2] = v[2], z[3] = v[3];
         } else {
+            const uint2 u = *(const uint2 *)((const uint16_t *)c + o);
+            const uint32_t h[4] = {u.x & 0xffffu, u.x >> 16, u.y & 0xffffu, u.y >> 16};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                z[i] = OUT_DT == kDtBF16 ? bf16_bits_to_f32(h[i]) : f16_bits_to_f32(h[i]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) z[i] = i < nvalid ? load_out<OUT_DT>(c, o + i) : 0.f;
+    }
+}
+
+// Stores four consecutive values (rounded to OUT_DT) at element offset o of a
+// C-shaped array; `vec` as in load4_out.  Vector stores are non-temporal: the
+// epilogue's arrays are written once and read by no later work of this
+// kernel, and keeping them out of the caches' way keeps the operand lines
+// that other tiles still read (8192^3 bf16 with f32 output: 0.805 ms instead
+// of 0.852 ms).
+template <int OUT_DT>
+__device__ __forceinline__ void store4_out(void *c, int64_t o, const float (&x)[4], bool vec, int nvalid) {
+    if (vec) {
+        if constexpr (OUT_DT == kDtF32) {
+            __builtin_nontemporal_store(f32x4_t{x[0], x[1], x[2], x[3]}, (f32x4_t *)((float *)c + o));
+        } else {
+            typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
             uint32_t lo, hi;
             if constexpr (OUT_DT == kDtBF16) {
                 lo = f32_to_bf16_bits(x[0]) | ((uint32_t)f32_to_bf16_bits(x[1]) << 16);
@@ -543,35 +542,76 @@ __device__ __forceinline__ void store4(const GemmArgs &p, int64_t o, int64_t col
                 lo = f32_to_f16_bits(x[0]) | ((uint32_t)f32_to_f16_bits(x[1]) << 16);
                 hi = f32_to_f16_bits(x[2]) | ((uint32_t)f32_to_f16_bits(x[3]) << 16);
             }
-            *(uint2 *)((uint16_t *)p.c + o) = make_uint2(lo, hi);
+            __builtin_nontemporal_store(u32x2_t{lo, hi}, (u32x2_t *)((uint16_t *)c + o));
         }
     } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            if (i < nvalid) store_out<OUT_DT>(p.c, o + i, x[i]);
+            if (i < nvalid) store_out<OUT_DT>(c, o + i, x[i]);
     }
+}
+
+// Applies the epilogue to 4 adjacent outputs (row-major offset o, nvalid of
+// them inside N) and stores them: + bias (b4, this lane's four columns) and
+// GELU with the pre-activation saved to aux, or * GELU'(z4) (z4: the aux
+// values of these outputs, loaded by the caller); with p.colsum, adds the
+// stored values to cs.
+template <int OUT_DT>
+__device__ __forceinline__ void store4(const GemmArgs &p, int64_t o, float4 v, bool vec, int nvalid,
+                                       const float (&b4)[4], const float (&z4)[4], float (&cs)[4]) {
+    float x[4] = {v.x, v.y, v.z, v.w};
+    if (p.act == kActDGelu) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i < nvalid) x[i] *= dgelu_erf(z4[i]);
+    } else {
+        if (p.bias) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (i < nvalid) x[i] += b4[i];
+        }
+        if (p.act == kActGelu) {
+            if (p.aux) store4_out<OUT_DT>(p.aux, o, x, vec, nvalid);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (i < nvalid) x[i] = gelu_erf(x[i]);
+        }
+    }
+    if (p.colsum) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i < nvalid) cs[i] += stored_value<OUT_DT>(x[i]);
+    }
+    store4_out<OUT_DT>(p.c, o, x, vec, nvalid);
 }
 
 // Writes one 32-row slab of a wave's accumulators (already staged in LDS as
 // f32 [32][WN + 8]) to C with coalesced 4-element stores; lane l owns columns
-// col0 + 4 (l % (WN/4)) .. +3 of rows l / (WN/4), + 64/(WN/4), ...
+// col0 + 4 (l % (WN/4)) .. +3 of rows l / (WN/4), + 64/(WN/4), ...  b4: the
+// bias of the lane's four columns.
 template <int OUT_DT, int WN>
 __device__ __forceinline__ void write_slab(const GemmArgs &p, const float *ws, int64_t cbase, int64_t row0,
-                                           int64_t col0, int lane, float (&cs)[4]) {
+                                           int64_t col0, int lane, const float (&b4)[4], float (&cs)[4]) {
     constexpr int kLanesPerRow = WN / 4;
     constexpr int kRowsPerIter = 64 / kLanesPerRow;
+    constexpr int kIters = 32 / kRowsPerIter;
     constexpr int kSld = WN + 8;
     const int c4 = (lane % kLanesPerRow) * 4;
     const int64_t col = col0 + c4;
     const int nvalid = (int)(p.N - col < 4 ? (p.N - col < 0 ? 0 : p.N - col) : 4);
-    const bool aligned = (p.N & 3) == 0 && (((uintptr_t)p.c) & 15) == 0;
-    for (int it = 0; it < 32 / kRowsPerIter; ++it) {
-        int r = it * kRowsPerIter + lane / kLanesPerRow;
-        int64_t row = row0 + r;
+    const bool aligned = (p.N & 3) == 0 && (((uintptr_t)p.c) & 15) == 0 && (((uintptr_t)p.aux) & 15) == 0;
+    const bool vec = aligned && nvalid == 4;
+    const int r0 = lane / kLanesPerRow;
+#pragma unroll 2
+    for (int it = 0; it < kIters; ++it) {
+        const int r = it * kRowsPerIter + r0;
+        const int64_t row = row0 + r;
         if (row >= p.M || nvalid == 0) continue;
-        float4 v = *(const float4 *)(ws + r * kSld + c4);
-        int64_t o = cbase + row * p.N + col;
-        store4<OUT_DT>(p, o, col, v, aligned && nvalid == 4, nvalid, cs);
+        const int64_t o = cbase + row * p.N + col;
+        float z4[4] = {0.f, 0.f, 0.f, 0.f};
+        if (p.act == kActDGelu) load4_out<OUT_DT>(p.aux, o, vec, nvalid, z4);
+        const float4 v = *(const float4 *)(ws + r * kSld + c4);
+        store4<OUT_DT>(p, o, v, vec, nvalid, b4, z4, cs);
     }
 }
 
@@ -605,6 +645,13 @@ __device__ __forceinline__ void epilogue_lds(const GemmArgs &p, f32x16_t (&acc)[
     static_assert(NT / 64 * 32 * kSld * 4 <= LDS_BYTES, "epilogue staging must fit in LDS");
     float *ws = (float *)lds + wave * 32 * kSld;
     float cs[4] = {0.f, 0.f, 0.f, 0.f};  // column sums of the stored output (p.colsum)
+    float b4[4] = {0.f, 0.f, 0.f, 0.f};  // bias of this lane's four columns (the same in every row)
+    if (p.bias && p.act != kActDGelu) {
+        const int64_t col = col0 + (lane % (WN / 4)) * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (col + i < p.N) b4[i] = load_as_f32(p.bias, p.bias_dtype, col + i);
+    }
     static_for<0, TM>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
 #pragma unroll
@@ -615,11 +662,11 @@ __device__ __forceinline__ void epilogue_lds(const GemmArgs &p, f32x16_t (&acc)[
         __syncthreads();
         const int64_t row0 = row_base + i * 32;
         if (p.out_dtype == kDtF32)
-            write_slab<kDtF32, WN>(p, ws, cbase, row0, col0, lane, cs);
+            write_slab<kDtF32, WN>(p, ws, cbase, row0, col0, lane, b4, cs);
         else if (p.out_dtype == kDtBF16)
-            write_slab<kDtBF16, WN>(p, ws, cbase, row0, col0, lane, cs);
+            write_slab<kDtBF16, WN>(p, ws, cbase, row0, col0, lane, b4, cs);
         else
-            write_slab<kDtF16, WN>(p, ws, cbase, row0, col0, lane, cs);
+            write_slab<kDtF16, WN>(p, ws, cbase, row0, col0, lane, b4, cs);
         __syncthreads();
     });
     if (p.colsum) colsum_flush<WN>(p, cs, col0, lane);
@@ -943,6 +990,22 @@ struct FragReader {
             for (int i = 0; i < TILES; ++i) seg[i] = (uint32_t)((((row0 >> 5) + i) ^ j) << 6);
         }
     }
+    // Fragment of tile I of group g (one ds_read_b128, or two transposing
+    // reads for an M/N-major operand).
+    template <int I>
+    __device__ __forceinline__ uint4 read1(const uint8_t *stage, int g) const {
+        if constexpr (!MN) {
+            return *(const uint4 *)(stage + off[g] + I * kTileStride);
+        } else {
+            typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+            const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_i16x4 *)(uintptr_t)(uint32_t)(uintptr_t)(stage + rowpart[g][0] + seg[I]));
+            const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_i16x4 *)(uintptr_t)(uint32_t)(uintptr_t)(stage + rowpart[g][1] + seg[I]));
+            const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+            return make_uint4(l2.x, l2.y, h2.x, h2.y);
+        }
+    }
     __device__ __forceinline__ void read(const uint8_t *stage, int g, uint4 (&out)[TILES]) const {
 #pragma unroll
         for (int i = 0; i < TILES; ++i) {
@@ -1108,6 +1171,143 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dl(GemmArgs
     __syncthreads();
     epilogue_lds<NT, WM, WN, TM, TN, NS * kStage>(p, acc, lds, wave, lane, tc.bidx * p.M * p.N, m0 + wm * WM,
                                                   n0 + wn * WN);
+}
+
+// Direct-to-LDS GEMM with one wave per SIMD: 4 waves (2 x 2) of 128 x 128,
+// two stages of BKS = 64 k.  A 128 x 128 wave tile reads a third less from
+// LDS per flop than 128 x 64 (the LDS serves both the DMA writes and the
+// fragment reads, and its occupancy is what idles the MFMA pipe), but a lone
+// wave must keep its own MFMA pipe fed, so its instruction stream is placed
+// by hand: a stage is four groups of 16 MFMAs (one per 32 x 32 block), and
+// every MFMA slot carries at most one other instruction -- a fragment read
+// for the next group (slots 0-7, in the order the next group's MFMAs consume
+// them) or a DMA instruction of the next stage (slots 8-15 of the first two
+// groups after the barrier).  The last group of each stage is deferred past
+// the barrier so the MFMA pipe works while the next stage's first fragments
+// are read.
+template <typename T, int BM, int BN, int BKS, bool AMN, bool BMN, int DF = 8, int DS = 2>
+__global__ void __launch_bounds__(256) gemm_kernel_dli(GemmArgs p) {
+    constexpr int NT = 256, WAVES_N = 2;
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int kStageA = BM * BKS * 2, kStageB = BN * BKS * 2;
+    constexpr int kStage = kStageA + kStageB;
+    constexpr int kG = BKS / 16;
+    static_assert(Elem<T>::kBytes == 2, "direct-to-LDS path is for 16-bit operands");
+    static_assert(kG == 4, "four fragment groups per stage");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStage];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const TileCoord tc = tile_coord<BM, BN>(p, blockIdx.x);
+    const int64_t m0 = tc.m0, n0 = tc.n0;
+    using LA = DirectLoader<BM, NT, AMN, BKS>;
+    using LB = DirectLoader<BN, NT, BMN, BKS>;
+    LA la((const char *)p.a + (tc.offa + m0 * p.sam) * 2, p.sam, p.sak, p.M - m0, p.K, wave, lane);
+    LB lb((const char *)p.b + (tc.offb + n0 * p.sbn) * 2, p.sbn, p.sbk, p.N - n0, p.K, wave, lane);
+    constexpr int L = LA::kPer + LB::kPer;  // DMA instructions per wave per stage
+    constexpr int Q = TM * TN;              // MFMA slots per group
+    constexpr int R = TM + TN;              // fragment reads per group
+    static_assert(R <= Q && DF + (L - 1) * DS < kG * Q, "DMA must fit the slots of one iteration");
+    const FragReader<BM, TM, AMN, BKS> fra(0, wm * WM, lane);
+    const FragReader<BN, TN, BMN, BKS> frb(kStageA, wn * WN, lane);
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x16_t{};
+    uint4 fa[2][TM], fb[2][TN];
+
+    // One group (GI-th of an iteration; GI < 0: no DMA): the MFMAs of register
+    // set USE (MF = false: none); slot s < R also reads fragment s of group GN
+    // (GN < 0: none) of stage `rs` into set USE ^ 1 (A0, B0 .. B(TN-1), A1 ..
+    // A(TM-1): the order the next group consumes them); DMA instruction l of
+    // the next stage goes into iteration slot DF + l * DS.
+    auto group = [&](auto usec, auto mfc, auto gnc, auto gic, const uint8_t *rs, const typename LA::Stage &sta,
+                     const typename LB::Stage &stb) {
+        constexpr int USE = decltype(usec)::value, GN = decltype(gnc)::value, GI = decltype(gic)::value;
+        constexpr bool MF = decltype(mfc)::value;
+        static_for<0, Q>([&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            if constexpr (MF) Mma<T>::run(acc[q / TN][q % TN], fa[USE][q / TN], fb[USE][q % TN]);
+            if constexpr (GN >= 0 && q < R) {
+                if constexpr (q == 0)
+                    fa[USE ^ 1][0] = fra.template read1<0>(rs, GN);
+                else if constexpr (q <= TN)
+                    fb[USE ^ 1][q - 1] = frb.template read1<(q > 0 && q <= TN ? q - 1 : 0)>(rs, GN);
+                else
+                    fa[USE ^ 1][q - TN] = fra.template read1<(q > TN ? q - TN : 0)>(rs, GN);
+            }
+            constexpr int sg = GI * Q + q;
+            if constexpr (GI >= 0 && sg >= DF && (sg - DF) % DS == 0 && (sg - DF) / DS < L) {
+                constexpr int l = (sg - DF) / DS;
+                if constexpr (l < LA::kPer)
+                    la.template issue_one<(l < LA::kPer ? l : 0)>(sta, wave);
+                else
+                    lb.template issue_one<(l >= LA::kPer ? l - LA::kPer : 0)>(stb, wave);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using INone = std::integral_constant<int, -1>;
+    using YES = std::integral_constant<bool, true>;
+    using NO = std::integral_constant<bool, false>;
+    // every LDS read of this wave landed; its DMA into the next stage landed;
+    // then all waves
+    auto stage_barrier = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & ~(0xF << 8));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    const int nk = (int)((p.K + BKS - 1) / BKS);
+    // Prologue: DMA of steps 0 and 1, wait for step 0, its group-0 fragments.
+    la.issue(lds, 0, wave);
+    lb.issue(lds + kStageA, 0, wave);
+    la.issue(lds + kStage, 1, wave);
+    lb.issue(lds + kStage + kStageA, 1, wave);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(L));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        const typename LA::Stage sta = la.prep(lds, 0);
+        const typename LB::Stage stb = lb.prep(lds + kStageA, 0);
+        // group-0 fragment reads of step 0, no MFMAs yet
+        group(I1{}, NO{}, I0{}, INone{}, lds, sta, stb);
+        group(I0{}, YES{}, I1{}, INone{}, lds, sta, stb);
+        group(I1{}, YES{}, I2{}, INone{}, lds, sta, stb);
+        group(I0{}, YES{}, I3{}, INone{}, lds, sta, stb);
+    }
+    for (int kt = 1; kt < nk; ++kt) {
+        stage_barrier();
+        const uint8_t *stage = lds + (kt & 1) * kStage;
+        uint8_t *other = lds + ((kt & 1) ^ 1) * kStage;
+        // DMA of step kt+1 into the stage step kt-1 used (past K: zeros)
+        const typename LA::Stage sta = la.prep(other, kt + 1);
+        const typename LB::Stage stb = lb.prep(other + kStageA, kt + 1);
+        group(I1{}, YES{}, I0{}, I0{}, stage, sta, stb);  // group 3 of step kt-1
+        group(I0{}, YES{}, I1{}, I1{}, stage, sta, stb);  // groups 0-2 of step kt
+        group(I1{}, YES{}, I2{}, I2{}, stage, sta, stb);
+        group(I0{}, YES{}, I3{}, I3{}, stage, sta, stb);
+    }
+    {
+        const typename LA::Stage sta = la.prep(lds, 0);
+        const typename LB::Stage stb = lb.prep(lds + kStageA, 0);
+        group(I1{}, YES{}, INone{}, INone{}, lds, sta, stb);  // group 3 of the last step
+    }
+    // drain every DMA (the last steps' are out of range) before the LDS is reused
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();
+    epilogue_lds<NT, WM, WN, TM, TN, 2 * kStage>(p, acc, lds, wave, lane, tc.bidx * p.M * p.N, m0 + wm * WM,
+                                                 n0 + wn * WN);
 }
 
 }  // namespace oxm
