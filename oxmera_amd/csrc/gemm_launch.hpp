@@ -14,9 +14,7 @@ enum LoaderKind : int { kLdK = 0, kLdMN = 1, kLdG = 2, kLdKR = 3, kLdMNR = 4 };
 // Tile configurations.
 enum TileCfg : int {
     kCfgF32_128 = 0,   // f32: 128x128 tile, 2x2 waves of 64x64, BK 32
-    kCfgH_256 = 1,     // bf16/f16: 256x256 tile, direct-to-LDS, BK 64: one wave per SIMD (2x2 waves of
-                       // 128x128, kCfgH_256_1W) when the epilogue is a plain store, else 2x4 waves of
-                       // 128x64 (kCfgH_256_8W)
+    kCfgH_256 = 1,     // bf16/f16: 256x256 tile, 2x4 waves of 128x64 (direct-to-LDS), BK 64
     kCfgH_128 = 2,     // bf16/f16: 128x128 tile, 2x2 waves of 64x64, BK 64
                        // (K- or M/N-contiguous operands use the direct-to-LDS kernel:
                        //  2 stages of 64 k, 128-byte rows)
@@ -26,7 +24,6 @@ enum TileCfg : int {
     kCfgF32_256 = 5,   // f32: 256x256 tile, 2x4 waves of 128x64, BK 32 (problems of >= 256 tiles)
     kCfgH_256_1W = 6,  // 16-bit direct-to-LDS 256x256, 2x2 waves of 128x128, one wave per SIMD,
                        // hand-interleaved MFMA / fragment-read / DMA stream
-    kCfgH_256_8W = 7,  // 16-bit direct-to-LDS 256x256, 2x4 waves of 128x64, whatever the epilogue
 };
 
 struct TileShape {

@@ -538,8 +538,7 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     } else {
         cfg = big ? oxm::kCfgH_256 : oxm::kCfgH_128;
         cfg = env_int("OXM_GEMM_CFG", cfg);
-        if ((cfg < oxm::kCfgH_256 || cfg > oxm::kCfgH_256_NS) && cfg != oxm::kCfgH_256_1W && cfg != oxm::kCfgH_256_8W)
-            cfg = oxm::kCfgH_128;
+        if ((cfg < oxm::kCfgH_256 || cfg > oxm::kCfgH_256_NS) && cfg != oxm::kCfgH_256_1W) cfg = oxm::kCfgH_128;
     }
     oxm::TileShape ts = oxm::tile_shape(cfg);
     int ld_a = classify((const char *)g.a, g.sam, g.sak, M, K, g.bsa, nbd, es, ts.bm);

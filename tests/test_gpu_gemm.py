@@ -113,6 +113,33 @@ def test_layouts_full(hip, dtype, la, lb):
         assert_close(to_f32(c), ref, spec_tolerance(dtype, k), f"{dtype.name} {la}x{lb} {m}x{k}x{n}")
 
 
+# ---- every 16-bit tile configuration on edge shapes ---------------------------------
+# The dispatcher gives 256x256 tiles only to problems of >= ~256 tiles, so at
+# the sizes above every 16-bit GEMM runs 128x128 tiles.  OXM_GEMM_CFG (read by
+# the library at each call) forces each configuration onto small shapes with
+# ragged edge tiles in M and N and a K tail: 1 = 256x256 direct-to-LDS, 2x4
+# waves (the default for large problems); 3 = the same with 2x2 waves; 4 =
+# 256x256 register-staged; 6 = 256x256 direct-to-LDS with one wave per SIMD
+# and a hand-placed instruction stream; 2 = 128x128.
+TILE_CFGS = {"256": 1, "256_4w": 3, "256_regstaged": 4, "256_1w": 6, "128": 2}
+EDGE_SHAPES = [(300, 200, 264), (264, 136, 520), (64, 72, 64), (520, 64, 8)]
+
+
+@pytest.mark.parametrize("cfg", list(TILE_CFGS))
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("la,lb", [("row", "col"), ("row", "row"), ("col", "col"), ("colgap", "row"),
+                                   ("gather", "col")])
+def test_tile_configs_16bit(hip, monkeypatch, cfg, dtype, la, lb):
+    monkeypatch.setenv("OXM_GEMM_CFG", str(TILE_CFGS[cfg]))
+    for si, (m, k, n) in enumerate(EDGE_SHAPES):
+        a = make_operand(dtype, la, m, k, 3000 + si, "a")
+        b = make_operand(dtype, lb, k, n, 4000 + si, "b")
+        log(f"tile cfg {cfg} {dtype.name} {la}x{lb} M={m} K={k} N={n}")
+        c = hip.matmul(a.dev, b.dev)
+        assert_close(to_f32(c), O.matmul(a.ora, b.ora), spec_tolerance(dtype, k),
+                     f"cfg {cfg} {dtype.name} {la}x{lb} {m}x{k}x{n}")
+
+
 RAGGED = [(5, 3, 7), (129, 13, 131), (300, 257, 259), (257, 1, 6), (70, 130, 65), (33, 66, 1)]
 
 
@@ -186,9 +213,22 @@ def test_zero_sized_and_k_zero(hip):
 
 # ---- epilogues --------------------------------------------------------------------
 
+# cfg: None = the dispatcher's choice; "1" / "6" force the 256x256 2x4-wave and
+# one-wave-per-SIMD 16-bit kernels (OXM_GEMM_CFG), whose epilogues differ in
+# wave tile (128x64 / 128x128)
+EPI_CFGS = [None, "1", "6"]
+
+
+def _force_cfg(monkeypatch, cfg):
+    if cfg is not None:
+        monkeypatch.setenv("OXM_GEMM_CFG", cfg)
+
+
+@pytest.mark.parametrize("cfg", EPI_CFGS, ids=["auto", "cfg1", "cfg6"])
 @pytest.mark.parametrize("dtype,out", [(F32, F32), (BF16, F32), (BF16, BF16), (F16, F16)],
                          ids=["f32", "bf16-f32", "bf16-bf16", "f16-f16"])
-def test_bias_gelu_epilogue(hip, dtype, out):
+def test_bias_gelu_epilogue(hip, monkeypatch, dtype, out, cfg):
+    _force_cfg(monkeypatch, cfg)
     rng = np.random.default_rng(21)
     m, k, n = 130, 192, 200
     a = contiguous_operand(dtype, rng.normal(0, 1, (m, k)))
@@ -209,8 +249,10 @@ def test_bias_gelu_epilogue(hip, dtype, out):
     assert_close(to_f32(c), widen(ref), tol, "gelu output")
 
 
+@pytest.mark.parametrize("cfg", EPI_CFGS, ids=["auto", "cfg1", "cfg6"])
 @pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
-def test_dgelu_epilogue(hip, dtype):
+def test_dgelu_epilogue(hip, monkeypatch, dtype, cfg):
+    _force_cfg(monkeypatch, cfg)
     rng = np.random.default_rng(31)
     m, k, n = 96, 160, 130
     a = contiguous_operand(dtype, rng.normal(0, 1, (m, k)))
@@ -237,10 +279,12 @@ def _check_colsum(cs: ox.Tensor, out: np.ndarray, what: str):
     assert worst <= 1.0, f"{what}: column sum off by {worst:.3g} x the f32 summation bound"
 
 
+@pytest.mark.parametrize("cfg", EPI_CFGS, ids=["auto", "cfg1", "cfg6"])
 @pytest.mark.parametrize("case", ["f32", "f32_ragged", "bf16_dgelu", "bf16_gelu_bf16out", "f32_batched",
                                   "bf16_256tiles"])
-def test_epilogue_column_sums(hip, case):
+def test_epilogue_column_sums(hip, monkeypatch, case, cfg):
     """colsum = sums over rows (and batches) of the output as stored."""
+    _force_cfg(monkeypatch, cfg)
     rng = np.random.default_rng(41)
     d = ox.Device.rocm(0)
     kw = {}
