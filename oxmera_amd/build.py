@@ -22,7 +22,8 @@ BUILD = PKG / "_build"
 LIB = PKG / "liboxm.so"
 ARCH = os.environ.get("OXM_GFX", "gfx950")
 
-SOURCES = ["oxm_capi.cpp", "gemm.hip", "gemm_f32.hip", "gemm_bf16.hip", "gemm_f16.hip", "glue.hip", "elementwise.hip"]
+SOURCES = ["oxm_capi.cpp", "gemm.hip", "gemm_f32.hip", "gemm_bf16.hip", "gemm_f16.hip", "gemm_strip.hip",
+           "glue.hip", "elementwise.hip"]
 
 # -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 on this pool.
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",

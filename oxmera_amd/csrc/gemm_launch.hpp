@@ -31,6 +31,15 @@ struct TileShape {
 };
 TileShape tile_shape(int cfg);
 
+// Row strip: at most this many leftover rows of a GEMM run on the strip
+// kernel (gemm_strip.hip) instead of a round of mostly empty 256x256 tiles.
+constexpr int kStripMaxRows = 16;
+
+// C[0..M) = A[0..M) . B for a strip of M <= kStripMaxRows rows, one batch, a
+// plain store epilogue (no bias, activation or column sums); `args` is
+// validated by the caller.
+hipError_t launch_gemm_strip(const GemmArgs &args, int dtype, hipStream_t stream);
+
 // Launch one batched GEMM.  `args` must be fully validated by the caller;
 // tiles_m/tiles_n/group_m/xcd_remap are filled in here.
 hipError_t launch_gemm(GemmArgs args, int dtype, int ld_a, int ld_b, int cfg, hipStream_t stream);

@@ -529,8 +529,23 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     g.out_dtype = c->dtype;
     g.bias_dtype = ep->bias_dtype;
 
+    // Row strip: when the last M % 256 rows alone would cost one more round
+    // of 256x256 tiles (4097 x 4095: 16 tile-rows fill the CUs once, the 17th
+    // holds one row), the whole 256-row tiles run as usual and those rows run
+    // on the strip kernel, which reads B once with plain FMAs (one batch, a
+    // plain store epilogue).
+    int64_t strip = 0;
+    if (batch == 1 && ep->act == OXM_ACT_NONE && !ep->bias && !ep->colsum && M > 256) {
+        const int64_t rem = M % 256, tn = (N + 255) / 256;
+        const int64_t full = ((M + 255) / 256) * tn, bulk = (M / 256) * tn;
+        if (rem <= oxm::kStripMaxRows && (full + 255) / 256 > (bulk + 255) / 256 && prefer_256_tiles(M - rem, N, 1))
+            strip = rem;
+    }
+    const int64_t Mt = M - strip;  // rows on MFMA tiles
+    g.M = Mt;
+
     int cfg;
-    const bool big = prefer_256_tiles(M, N, batch);
+    const bool big = prefer_256_tiles(Mt, N, batch);
     if (a->dtype == OXM_F32) {
         cfg = big ? oxm::kCfgF32_256 : oxm::kCfgF32_128;
         cfg = env_int("OXM_GEMM_CFG_F32", cfg);
@@ -541,9 +556,13 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
         if ((cfg < oxm::kCfgH_256 || cfg > oxm::kCfgH_256_NS) && cfg != oxm::kCfgH_256_1W) cfg = oxm::kCfgH_128;
     }
     oxm::TileShape ts = oxm::tile_shape(cfg);
-    int ld_a = classify((const char *)g.a, g.sam, g.sak, M, K, g.bsa, nbd, es, ts.bm);
+    if (strip && ts.bm != 256) {  // a forced 128x128 configuration: no strip
+        strip = 0;
+        g.M = M;
+    }
+    int ld_a = classify((const char *)g.a, g.sam, g.sak, g.M, K, g.bsa, nbd, es, ts.bm);
     int ld_b = classify((const char *)g.b, g.sbn, g.sbk, N, K, g.bsb, nbd, es, ts.bn);
-    int64_t ntiles = ((M + ts.bm - 1) / ts.bm) * ((N + ts.bn - 1) / ts.bn) * batch;
+    int64_t ntiles = ((g.M + ts.bm - 1) / ts.bm) * ((N + ts.bn - 1) / ts.bn) * batch;
     if (ntiles > 0x7fffffffLL) return fail(OXM_E_NOT_IMPLEMENTED, "matmul is not implemented for %lld tiles", (long long)ntiles);
     hipStream_t s = (hipStream_t)stream;
     if (ep->colsum) {
@@ -553,6 +572,14 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     }
     hipError_t e = oxm::launch_gemm(g, a->dtype, ld_a, ld_b, cfg, s);
     if (e != hipSuccess) return hip_fail(e, op);
+    if (strip) {
+        oxm::GemmArgs gs = g;
+        gs.M = strip;
+        gs.a = (const char *)g.a + g.M * g.sam * es;
+        gs.c = (char *)g.c + g.M * N * oes;
+        e = oxm::launch_gemm_strip(gs, a->dtype, s);
+        if (e != hipSuccess) return hip_fail(e, op);
+    }
     return finish(s, op);
 }
 

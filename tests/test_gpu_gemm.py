@@ -140,6 +140,40 @@ def test_tile_configs_16bit(hip, monkeypatch, cfg, dtype, la, lb):
                      f"cfg {cfg} {dtype.name} {la}x{lb} {m}x{k}x{n}")
 
 
+# ---- row strip: the leftover rows of a 256x256-tiled GEMM ----------------------------
+# M = 2048 + r with N = 8192: 8 tile-rows x 32 tile-columns fill the 256 CUs
+# once, so r <= 16 leftover rows run on the strip kernel instead of a second,
+# mostly empty round of tiles (r = 17 does take the second round).  Checked
+# on the strip rows, the rows either side of the split, and a few others.
+STRIP_CASES = [  # dtype, out dtype, A layout, B layout, M, K, N
+    (F32, F32, "row", "row", 2049, 72, 8192),
+    (F32, F32, "flip", "row", 2051, 100, 8190),   # 16-byte loads of B, straddling chunk at N
+    (F32, F32, "row", "col", 2050, 52, 8188),     # B not N-contiguous: element loads
+    (BF16, F32, "row", "col", 2051, 136, 8192),
+    (BF16, BF16, "gather", "col", 2064, 64, 8192),
+    (F16, F16, "flip", "row", 2053, 40, 8192),
+    (F16, F16, "row", "row", 2065, 40, 8192),
+]
+
+
+@pytest.mark.parametrize("case", range(len(STRIP_CASES)))
+def test_row_strip(hip, case):
+    dtype, out, la, lb, m, k, n = STRIP_CASES[case]
+    a = make_operand(dtype, la, m, k, 50 + case, "a")
+    b = make_operand(dtype, lb, k, n, 60 + case, "b")
+    log(f"row strip {dtype.name}->{out.name} {la}x{lb} M={m} K={k} N={n}")
+    c = to_f32(hip.matmul(a.dev, b.dev, out_dtype=out)).reshape(m, n)
+    rows = np.unique(np.concatenate([np.arange(2040, m), [0, 1, 777, 1500]])).astype(np.int64)
+    odt = {F32: O.F32, BF16: O.BF16, F16: O.F16}[out]
+    ref = O.matmul(a.ora, b.ora, rows=rows, out_dtype=odt)
+    if out == BF16:
+        ref = O.bf16_to_f32(ref)
+    elif out == F16:
+        ref = ref.view(np.float16).astype(np.float32)
+    tol = spec_tolerance(dtype, k) if out == F32 else 1e-2
+    assert_close(c[rows], ref, tol, f"strip case {case}")
+
+
 RAGGED = [(5, 3, 7), (129, 13, 131), (300, 257, 259), (257, 1, 6), (70, 130, 65), (33, 66, 1)]
 
 
