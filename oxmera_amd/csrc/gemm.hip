@@ -18,6 +18,7 @@ TileShape tile_shape(int cfg) {
     case kCfgH_256_NS:
     case kCfgF32_256: return {256, 256};
     case kCfgH_128: return {128, 128};
+    case kCfgF32_64: return {64, 64};
     default: return {128, 128};
     }
 }

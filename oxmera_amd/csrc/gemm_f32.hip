@@ -5,6 +5,7 @@ namespace oxm {
 
 hipError_t launch_gemm_f32(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipStream_t s) {
     if (cfg == kCfgF32_256) return pick_a_f32<256, 256, 2, 4>(a, ld_a, ld_b, s);
+    if (cfg == kCfgF32_64) return pick_a_f32<64, 64, 2, 2>(a, ld_a, ld_b, s);
     return pick_a_f32<128, 128, 2, 2>(a, ld_a, ld_b, s);
 }
 

@@ -547,9 +547,12 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     int cfg;
     const bool big = prefer_256_tiles(Mt, N, batch);
     if (a->dtype == OXM_F32) {
-        cfg = big ? oxm::kCfgF32_256 : oxm::kCfgF32_128;
+        // f32 problems of at most 64 128x128 tiles (a quarter of the CUs)
+        // take 64x64 tiles: 256^3 runs on 16 CUs instead of 4
+        const int64_t n128 = ((Mt + 127) / 128) * ((N + 127) / 128) * batch;
+        cfg = big ? oxm::kCfgF32_256 : (n128 <= 64 ? oxm::kCfgF32_64 : oxm::kCfgF32_128);
         cfg = env_int("OXM_GEMM_CFG_F32", cfg);
-        if (cfg != oxm::kCfgF32_256) cfg = oxm::kCfgF32_128;
+        if (cfg != oxm::kCfgF32_256 && cfg != oxm::kCfgF32_64) cfg = oxm::kCfgF32_128;
     } else {
         cfg = big ? oxm::kCfgH_256 : oxm::kCfgH_128;
         cfg = env_int("OXM_GEMM_CFG", cfg);

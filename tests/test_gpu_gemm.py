@@ -140,6 +140,27 @@ def test_tile_configs_16bit(hip, monkeypatch, cfg, dtype, la, lb):
                      f"cfg {cfg} {dtype.name} {la}x{lb} {m}x{k}x{n}")
 
 
+# f32 the same way (OXM_GEMM_CFG_F32): 0 = 128x128, 5 = 256x256, 8 = 64x64 (the
+# dispatcher's choice for problems of at most 64 128x128 tiles), over every
+# loader kind the f32 kernels have, ragged rows included.
+F32_TILE_CFGS = {"128": 0, "256": 5, "64": 8}
+F32_EDGE_SHAPES = [(300, 200, 264), (129, 133, 131), (64, 72, 64), (33, 257, 70)]
+
+
+@pytest.mark.parametrize("cfg", list(F32_TILE_CFGS))
+@pytest.mark.parametrize("la,lb", [("row", "row"), ("row", "col"), ("col", "row"), ("gather", "flip"),
+                                   ("colgap", "colgap")])
+def test_tile_configs_f32(hip, monkeypatch, cfg, la, lb):
+    monkeypatch.setenv("OXM_GEMM_CFG_F32", str(F32_TILE_CFGS[cfg]))
+    for si, (m, k, n) in enumerate(F32_EDGE_SHAPES):
+        a = make_operand(F32, la, m, k, 5000 + si, "a")
+        b = make_operand(F32, lb, k, n, 6000 + si, "b")
+        log(f"f32 tile cfg {cfg} {la}x{lb} M={m} K={k} N={n}")
+        c = hip.matmul(a.dev, b.dev)
+        assert_close(to_f32(c), O.matmul(a.ora, b.ora), spec_tolerance(F32, k),
+                     f"f32 cfg {cfg} {la}x{lb} {m}x{k}x{n}")
+
+
 # ---- row strip: the leftover rows of a 256x256-tiled GEMM ----------------------------
 # M = 2048 + r with N = 8192: 8 tile-rows x 32 tile-columns fill the 256 CUs
 # once, so r <= 16 leftover rows run on the strip kernel instead of a second,
