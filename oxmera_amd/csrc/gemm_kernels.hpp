@@ -633,6 +633,16 @@ __device__ __forceinline__ void colsum_flush(const GemmArgs &p, float (&cs)[4], 
     }
 }
 
+// Orders this wave's LDS accesses before and after it for all of the wave's
+// lanes (the epilogue's staging area is per wave, so no other wave is waited
+// for: waves write their slabs out independently; against block barriers
+// here it measured the same, within 0.3 %, on C3, C2, C4 and the MLP).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // LDS-staged epilogue: each wave writes its WM x WN accumulators one 32-row
 // slab at a time through a padded LDS slab (row stride WN + 8 floats,
 // conflict-free), then stores rows with 16-byte writes, applying the bias and
@@ -659,7 +669,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmArgs &p, f32x16_t (&acc)[
 #pragma unroll
             for (int e = 0; e < 16; ++e)
                 ws[(8 * (e >> 2) + 4 * half + (e & 3)) * kSld + j * 32 + (lane & 31)] = acc[i][j][e];
-        __syncthreads();
+        wave_sync();
         const int64_t row0 = row_base + i * 32;
         if (p.out_dtype == kDtF32)
             write_slab<kDtF32, WN>(p, ws, cbase, row0, col0, lane, b4, cs);
@@ -667,7 +677,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmArgs &p, f32x16_t (&acc)[
             write_slab<kDtBF16, WN>(p, ws, cbase, row0, col0, lane, b4, cs);
         else
             write_slab<kDtF16, WN>(p, ws, cbase, row0, col0, lane, b4, cs);
-        __syncthreads();
+        wave_sync();
     });
     if (p.colsum) colsum_flush<WN>(p, cs, col0, lane);
 }
