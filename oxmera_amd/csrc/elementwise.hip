@@ -306,6 +306,63 @@ __global__ void __launch_bounds__(256) copy_transpose(EwShape s, int p, U *dst, 
     }
 }
 
+// The same with 16-byte accesses on both sides, for 2- and 4-byte elements
+// (the launcher has checked that both pointers are 16-byte aligned, that both
+// extents and every stride other than the unit ones are multiples of the
+// vector width W, so every vector below is aligned and wholly in or out of
+// range).  A lane reads W consecutive p of one l and stores them as one
+// 16-byte chunk of LDS row l, the chunk index XORed with (l / W) % C (C =
+// chunks per 64-element row); a lane then gathers W consecutive l of one p
+// from the columns -- with the XOR, the W-row groups of a wave's lanes fall
+// on different banks -- and writes them as one 16-byte vector.
+template <typename U>
+__global__ void __launch_bounds__(256) copy_transpose_vec(EwShape s, int p, U *dst, const U *src) {
+    constexpr int W = 16 / sizeof(U);
+    constexpr int C = kTT / W;        // 16-byte chunks per tile row
+    constexpr int kRowsPass = 256 / C;
+    __shared__ __attribute__((aligned(16))) U tile[kTT * kTT];
+    const int L = s.ndim - 1;
+    const int64_t np_ = s.shape[p], nl = s.shape[L];
+    const int64_t tiles_p = (np_ + kTT - 1) / kTT, tiles_l = (nl + kTT - 1) / kTT;
+    int64_t b = blockIdx.x;
+    const int64_t tl = b % tiles_l;
+    b /= tiles_l;
+    const int64_t tp = b % tiles_p;
+    b /= tiles_p;
+    int64_t od = 0, os = 0;
+    for (int d = L - 1; d >= 0; --d) {
+        if (d == p) continue;
+        const int64_t c = b % s.shape[d];
+        b /= s.shape[d];
+        od += c * s.st[0][d];
+        os += c * s.st[1][d];
+    }
+    const int64_t p0 = tp * kTT, l0 = tl * kTT;
+    const int64_t sl = s.st[1][L], dp = s.st[0][p];
+    const int c = threadIdx.x % C, r = threadIdx.x / C;
+#pragma unroll
+    for (int k = 0; k < kTT / kRowsPass; ++k) {
+        const int l = r + k * kRowsPass;
+        if (l0 + l < nl && p0 + c * W < np_)
+            *(uint4 *)&tile[l * kTT + ((c ^ ((l / W) % C)) * W)] =
+                *(const uint4 *)&src[os + (p0 + c * W) + (l0 + l) * sl];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kTT / kRowsPass; ++k) {
+        const int pp = r + k * kRowsPass;  // this lane's p in the tile; c: its group of W l's
+        if (p0 + pp < np_ && l0 + c * W < nl) {
+            alignas(16) U v[W];
+#pragma unroll
+            for (int i = 0; i < W; ++i) {
+                const int l = c * W + i;
+                v[i] = tile[l * kTT + (((pp / W) ^ ((l / W) % C)) * W) + pp % W];
+            }
+            *(uint4 *)&dst[od + (p0 + pp) * dp + (l0 + c * W)] = *(const uint4 *)v;
+        }
+    }
+}
+
 // ---- dtype conversion --------------------------------------------------------------
 
 template <int DI, int DO>
@@ -336,22 +393,69 @@ __device__ __forceinline__ float unfused_mul(float a, float b) {
     return m;
 }
 
-// MODE 0: plain, 1: momentum, 2: Nesterov momentum.  Each f32 operation is
-// rounded on its own (no fused multiply-adds), so the result is reproducible
-// operation by operation.
+// One parameter's update: MODE 0 plain, 1 momentum, 2 Nesterov momentum.
+// Each f32 operation is rounded on its own (no fused multiply-adds), so the
+// result is reproducible operation by operation.
+template <int MODE, bool WD>
+__device__ __forceinline__ float sgd_one(float pv, float gv, float &vv, float lr, float mu, float wd) {
+    if constexpr (WD) gv = gv + unfused_mul(wd, pv);
+    if constexpr (MODE != 0) {
+        vv = unfused_mul(mu, vv) + gv;
+        gv = MODE == 2 ? gv + unfused_mul(mu, vv) : vv;
+    }
+    return pv - unfused_mul(lr, gv);
+}
+
+// Eight consecutive elements as f32: one 16-byte access for a 16-bit type,
+// two for f32 (i a multiple of 8, the pointer 16-byte aligned).
+template <int DT>
+__device__ __forceinline__ void ld8(const void *p, int64_t i, float (&v)[8]) {
+    if constexpr (DT == kDtF32) {
+        float a[4], b[4];
+        ld16<kDtF32>(p, i, a);
+        ld16<kDtF32>(p, i + 4, b);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = a[e], v[e + 4] = b[e];
+    } else {
+        ld16<DT>(p, i, v);
+    }
+}
+template <int DT>
+__device__ __forceinline__ void st8(void *p, int64_t i, const float (&v)[8]) {
+    if constexpr (DT == kDtF32) {
+        const float a[4] = {v[0], v[1], v[2], v[3]}, b[4] = {v[4], v[5], v[6], v[7]};
+        st16<kDtF32>(p, i, a);
+        st16<kDtF32>(p, i + 4, b);
+    } else {
+        st16<DT>(p, i, v);
+    }
+}
+
 template <int PDT, int GDT, int MODE, bool WD>
 __global__ void __launch_bounds__(256) sgd_kernel(int64_t n, void *p, const void *g, float *v, float lr, float mu,
                                                   float wd) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-        const float pv = El<PDT>::load(p, i);
-        float gv = El<GDT>::load(g, i);
-        if constexpr (WD) gv = gv + unfused_mul(wd, pv);
-        if constexpr (MODE != 0) {
-            const float vv = unfused_mul(mu, v[i]) + gv;
-            v[i] = vv;
-            gv = MODE == 2 ? gv + unfused_mul(mu, vv) : vv;
-        }
-        El<PDT>::store(p, i, pv - unfused_mul(lr, gv));
+        float vv = MODE != 0 ? v[i] : 0.f;
+        El<PDT>::store(p, i, sgd_one<MODE, WD>(El<PDT>::load(p, i), El<GDT>::load(g, i), vv, lr, mu, wd));
+        if constexpr (MODE != 0) v[i] = vv;
+    }
+}
+
+// The same with eight elements per thread and 16-byte accesses (n a multiple
+// of 8, every array 16-byte aligned: checked by the launcher).
+template <int PDT, int GDT, int MODE, bool WD>
+__global__ void __launch_bounds__(256) sgd_kernel_vec(int64_t n, void *p, const void *g, float *v, float lr,
+                                                      float mu, float wd) {
+    for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8; i < n;
+         i += (int64_t)gridDim.x * blockDim.x * 8) {
+        float pv[8], gv[8], vv[8];
+        ld8<PDT>(p, i, pv);
+        ld8<GDT>(g, i, gv);
+        if constexpr (MODE != 0) ld8<kDtF32>(v, i, vv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = sgd_one<MODE, WD>(pv[e], gv[e], vv[e], lr, mu, wd);
+        st8<PDT>(p, i, pv);
+        if constexpr (MODE != 0) st8<kDtF32>(v, i, vv);
     }
 }
 
@@ -503,6 +607,91 @@ __global__ void __launch_bounds__(256) reduce_cols(RedGeom g, const void *x, voi
         ws[(int64_t)s * g.n_out + o] = acc[0];
 }
 
+// Columns with 16-byte loads: as reduce_cols, but thread t takes V = 16 /
+// sizeof(elem) consecutive outputs (the launcher has checked that the
+// innermost kept dim is contiguous with a length that is a multiple of V,
+// and that every V-group of outputs starts 16-byte aligned for every reduced
+// element), one vector load per reduced element, the reduced offset computed
+// once per vector.  Per output the same order as reduce_cols: kRedU partials
+// over interleaved reduced elements, combined 0..kRedU-1.
+template <int DT, int OP>
+__global__ void __launch_bounds__(256) reduce_cols_vec(RedGeom g, const void *x, void *out, float *ws, int splits) {
+    constexpr int V = DT == kDtF32 ? 4 : 8;
+    const int64_t o = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
+    const int s = blockIdx.y;
+    if (o >= g.n_out) return;
+    const int64_t base = dims_offset(g.nk, g.kshape, g.kst, o);
+    const int64_t chunk = (g.n_red + splits - 1) / splits;
+    const int64_t r0 = s * chunk, r1 = r0 + chunk < g.n_red ? r0 + chunk : g.n_red;
+    float acc[kRedU][V];
+#pragma unroll
+    for (int u = 0; u < kRedU; ++u)
+#pragma unroll
+        for (int e = 0; e < V; ++e) acc[u][e] = red_identity<OP, float>();
+    for (int64_t r = r0; r < r1; r += kRedU) {
+        float v[kRedU][V];
+#pragma unroll
+        for (int u = 0; u < kRedU; ++u) {
+            if (r + u < r1) {
+                ld16<DT>(x, base + red_offset(g, r + u), v[u]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < V; ++e) v[u][e] = red_identity<OP, float>();
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kRedU; ++u)
+#pragma unroll
+            for (int e = 0; e < V; ++e) acc[u][e] = red_combine<OP, float>(acc[u][e], v[u][e]);
+    }
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+        float t = acc[0][e];
+#pragma unroll
+        for (int u = 1; u < kRedU; ++u) t = red_combine<OP, float>(t, acc[u][e]);
+        if (splits == 1)
+            El<DT>::store(out, o + e, t);
+        else
+            ws[(int64_t)s * g.n_out + o + e] = t;
+    }
+}
+
+// The finishing pass for the column schedule (ws[s * n_out + o]): 64
+// consecutive outputs per block, four threads per output; thread (o, q)
+// combines splits q, q + 4, q + 8, ... (kRedU loads in flight), then the
+// four partials of an output are combined in q order through LDS -- a fixed
+// order, so results do not depend on scheduling.  A wave reads 64
+// consecutive outputs of one split (coalesced).
+template <int DT, int OP>
+__global__ void __launch_bounds__(256) reduce_finish_cols(const typename El<DT>::Acc *ws, int64_t n_out, int splits,
+                                                          void *out) {
+    using A = typename El<DT>::Acc;
+    __shared__ A part[4][64];
+    const int ol = threadIdx.x % 64, q = threadIdx.x / 64;
+    const int64_t o = (int64_t)blockIdx.x * 64 + ol;
+    A acc = red_identity<OP, A>();
+    if (o < n_out) {
+        for (int s0 = q; s0 < splits; s0 += 4 * kRedU) {
+            A v[kRedU];
+#pragma unroll
+            for (int u = 0; u < kRedU; ++u) {
+                const int sp = s0 + 4 * u;
+                v[u] = sp < splits ? ws[(int64_t)sp * n_out + o] : red_identity<OP, A>();
+            }
+#pragma unroll
+            for (int u = 0; u < kRedU; ++u) acc = red_combine<OP, A>(acc, v[u]);
+        }
+    }
+    part[q][ol] = acc;
+    __syncthreads();
+    if (q == 0 && o < n_out) {
+        A t = part[0][ol];
+#pragma unroll
+        for (int k = 1; k < 4; ++k) t = red_combine<OP, A>(t, part[k][ol]);
+        El<DT>::store(out, o, t);
+    }
+}
+
 // out[o] = the splits' partials combined, in a fixed order.  stride_o /
 // stride_s address ws[o * stride_o + s * stride_s].  A thread per output,
 // kRedU partials in flight.
@@ -643,9 +832,26 @@ hipError_t red_launch(const RedGeom &g, const void *x, void *out, hipStream_t st
                                out, ws, (int)splits);
         if (splits > 1) finish(splits, (int64_t)1);
     } else {
-        hipLaunchKernelGGL((reduce_cols<DT, OP>), dim3((unsigned)((g.n_out + 255) / 256), (unsigned)splits), dim3(256), 0,
-                           st, g, x, out, ws, (int)splits);
-        if (splits > 1) finish((int64_t)1, g.n_out);
+        bool vec = false;
+        if constexpr (DT != kDtF64) {
+            // every V-group of consecutive outputs starts 16-byte aligned at
+            // every reduced element: x aligned, the innermost kept dim a
+            // multiple of V long, every other stride a multiple of V
+            constexpr int V = DT == kDtF32 ? 4 : 8;
+            vec = (uintptr_t)x % 16 == 0 && g.kshape[g.nk - 1] % V == 0;
+            for (int d = 0; d + 1 < g.nk; ++d) vec = vec && g.kst[d] % V == 0;
+            for (int d = 0; d < g.nr; ++d) vec = vec && g.rst[d] % V == 0;
+            if (vec)
+                hipLaunchKernelGGL((reduce_cols_vec<DT, OP>),
+                                   dim3((unsigned)((g.n_out / V + 255) / 256), (unsigned)splits), dim3(256), 0, st, g,
+                                   x, out, (float *)ws, (int)splits);
+        }
+        if (!vec)
+            hipLaunchKernelGGL((reduce_cols<DT, OP>), dim3((unsigned)((g.n_out + 255) / 256), (unsigned)splits),
+                               dim3(256), 0, st, g, x, out, ws, (int)splits);
+        if (splits > 1)
+            hipLaunchKernelGGL((reduce_finish_cols<DT, OP>), dim3((unsigned)((g.n_out + 63) / 64)), dim3(256), 0, st,
+                               ws, g.n_out, (int)splits, out);
     }
     e = hipGetLastError();
     if (ws) {
@@ -692,6 +898,24 @@ hipError_t launch_copy(int elem_bytes, const EwShape &s, void *dst, const void *
                                        ((s.shape[L] + kTT - 1) / kTT);
     if (p >= 0 && blocks <= INT32_MAX) {
         const dim3 g((unsigned)blocks);
+        if (elem_bytes == 2 || elem_bytes == 4) {
+            const int w = 16 / elem_bytes;
+            bool vec = (uintptr_t)dst % 16 == 0 && (uintptr_t)src % 16 == 0 && s.shape[p] % w == 0 &&
+                       s.shape[L] % w == 0;
+            for (int d = 0; d <= L; ++d) {
+                if (d != L) vec = vec && s.st[0][d] % w == 0;
+                if (d != p) vec = vec && s.st[1][d] % w == 0;
+            }
+            if (vec) {
+                if (elem_bytes == 2)
+                    hipLaunchKernelGGL(copy_transpose_vec<uint16_t>, g, dim3(256), 0, st, s, p, (uint16_t *)dst,
+                                       (const uint16_t *)src);
+                else
+                    hipLaunchKernelGGL(copy_transpose_vec<uint32_t>, g, dim3(256), 0, st, s, p, (uint32_t *)dst,
+                                       (const uint32_t *)src);
+                return hipGetLastError();
+            }
+        }
         switch (elem_bytes) {
         case 1: hipLaunchKernelGGL(copy_transpose<uint8_t>, g, dim3(256), 0, st, s, p, (uint8_t *)dst, (const uint8_t *)src); break;
         case 2: hipLaunchKernelGGL(copy_transpose<uint16_t>, g, dim3(256), 0, st, s, p, (uint16_t *)dst, (const uint16_t *)src); break;
@@ -725,20 +949,31 @@ hipError_t convert_from(int dto, const EwShape &s, void *dst, const void *src, h
     return hipGetLastError();
 }
 
+template <int PDT, int GDT, int MODE, bool WD>
+void sgd_go(int64_t n, void *p, const void *g, float *v, float lr, float mu, float wd, hipStream_t st) {
+    const bool vec = n % 8 == 0 && (uintptr_t)p % 16 == 0 && (uintptr_t)g % 16 == 0 &&
+                     (MODE == 0 || (uintptr_t)v % 16 == 0);
+    if (vec)
+        hipLaunchKernelGGL((sgd_kernel_vec<PDT, GDT, MODE, WD>), dim3(grid_for(n / 8)), dim3(256), 0, st, n, p, g, v,
+                           lr, mu, wd);
+    else
+        hipLaunchKernelGGL((sgd_kernel<PDT, GDT, MODE, WD>), dim3(grid_for(n)), dim3(256), 0, st, n, p, g, v, lr, mu,
+                           wd);
+}
+
 template <int PDT, int GDT>
 hipError_t sgd_typed(int64_t n, void *p, const void *g, float *v, float lr, float mu, float wd, bool nesterov,
                      hipStream_t st) {
-    const dim3 grid(grid_for(n)), block(256);
     const bool w = wd != 0.0f;
     if (mu == 0.0f) {
-        if (w) hipLaunchKernelGGL((sgd_kernel<PDT, GDT, 0, true>), grid, block, 0, st, n, p, g, v, lr, mu, wd);
-        else hipLaunchKernelGGL((sgd_kernel<PDT, GDT, 0, false>), grid, block, 0, st, n, p, g, v, lr, mu, wd);
+        if (w) sgd_go<PDT, GDT, 0, true>(n, p, g, v, lr, mu, wd, st);
+        else sgd_go<PDT, GDT, 0, false>(n, p, g, v, lr, mu, wd, st);
     } else if (!nesterov) {
-        if (w) hipLaunchKernelGGL((sgd_kernel<PDT, GDT, 1, true>), grid, block, 0, st, n, p, g, v, lr, mu, wd);
-        else hipLaunchKernelGGL((sgd_kernel<PDT, GDT, 1, false>), grid, block, 0, st, n, p, g, v, lr, mu, wd);
+        if (w) sgd_go<PDT, GDT, 1, true>(n, p, g, v, lr, mu, wd, st);
+        else sgd_go<PDT, GDT, 1, false>(n, p, g, v, lr, mu, wd, st);
     } else {
-        if (w) hipLaunchKernelGGL((sgd_kernel<PDT, GDT, 2, true>), grid, block, 0, st, n, p, g, v, lr, mu, wd);
-        else hipLaunchKernelGGL((sgd_kernel<PDT, GDT, 2, false>), grid, block, 0, st, n, p, g, v, lr, mu, wd);
+        if (w) sgd_go<PDT, GDT, 2, true>(n, p, g, v, lr, mu, wd, st);
+        else sgd_go<PDT, GDT, 2, false>(n, p, g, v, lr, mu, wd, st);
     }
     return hipGetLastError();
 }

@@ -202,9 +202,9 @@ def test_mse_of_a_shared_output(hip):
 @pytest.mark.parametrize("cfg", [dict(), dict(weight_decay=0.01), dict(momentum=0.9),
                                  dict(momentum=0.9, nesterov=True, weight_decay=0.05)],
                          ids=["plain", "wd", "momentum", "nesterov-wd"])
-def test_sgd_bit_exact(hip, pdt, gdt, cfg):
+@pytest.mark.parametrize("n", [10007, 10008], ids=["n-odd", "n-vec"])  # 10008: the 8-per-thread vector kernel
+def test_sgd_bit_exact(hip, pdt, gdt, cfg, n):
     rng = np.random.default_rng(77)
-    n = 10007
     odt = {ox.DType.F32: O.F32, ox.DType.BF16: O.BF16, ox.DType.F16: O.F16}
     p0 = rng.normal(0, 1, n).astype(np.float32)
     p_raw = O.bf16_round(p0) if pdt == ox.DType.BF16 else p0.astype(np.float16 if pdt == ox.DType.F16 else np.float32)

@@ -220,5 +220,22 @@ def test_contiguous(hip, dtype):
         elif dtype == ox.DType.F16:
             gotv = gotv.astype(np.float16)
         assert np.array_equal(np.ascontiguousarray(gotv).view(np.uint8), ref.view(np.uint8)), perm
+    # tiled transposes with 16-byte vectors on both sides (2- and 4-byte
+    # elements: extents multiples of 8, tiles ragged, a batch dim); 8-byte
+    # elements take the element-wise tile
+    if dtype == ox.DType.I32:
+        buf3 = rng.integers(-1000, 1000, 2 * 96 * 136).astype(np.int32)
+    else:
+        buf3 = raw(rng.normal(0, 1, 2 * 96 * 136), DT[dtype])
+    base3 = ox.Tensor.from_numpy(buf3, d, dtype).reshape((2, 96, 136))
+    for perm in [(0, 2, 1), (2, 1, 0), (1, 2, 0)]:
+        c = base3.permute(list(perm)).contiguous()
+        ref = np.ascontiguousarray(np.transpose(buf3.reshape(2, 96, 136), perm))
+        gotv = c.to_numpy()
+        if dtype == ox.DType.BF16:
+            gotv = R.from_f32(gotv, R.BF16)
+        elif dtype == ox.DType.F16:
+            gotv = gotv.astype(np.float16)
+        assert np.array_equal(np.ascontiguousarray(gotv).view(np.uint8), ref.view(np.uint8)), ("vec", perm)
     same = base.contiguous()
     assert same.data_ptr() == base.data_ptr()                         # a no-op clone when contiguous
