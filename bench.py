@@ -469,7 +469,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the GEMM would shard by rows "
-              "of A/C, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "of A and C, each GPU running the same kernel on its share); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     if args.workload == "mlp":
