@@ -773,8 +773,9 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
     // compiler sinks the global loads next to their LDS stores and exposes
     // the full memory latency every step):
     //   global loads of step kt+PF
-    //   for g = 0..3: LDS reads of group g+1, MFMAs of group g
-    //   LDS stores of step kt+1, barrier, LDS reads of group 0 of kt+1.
+    //   for g = 0..2: LDS reads of group g+1, MFMAs of group g
+    //   LDS stores of step kt+1, barrier, LDS reads of group 0 of kt+1,
+    //   MFMAs of group 3 (under the latency of those reads).
     // Loads past the end of K are out of range and read zeros.
     static_assert(PF == 1 || PF == 2, "prefetch distance 1 or 2");
     const int nk = (int)((p.K + kBK - 1) / kBK);
@@ -799,9 +800,9 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
         la.template prefetch<kLoadSet>(kt + PF);
         lb.template prefetch<kLoadSet>(kt + PF);
         if constexpr (SCHED) __builtin_amdgcn_sched_barrier(0);
-        static_for<0, 4>([&](auto gc) {
+        static_for<0, 3>([&](auto gc) {
             constexpr int g = decltype(gc)::value;
-            if constexpr (g < 3) read_frags(stage, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
+            read_frags(stage, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -811,7 +812,15 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
         la.template store<kStoreSet>(nxt, tid, kt + 1);
         lb.template store<kStoreSet>(nxt + kRegionA, tid, kt + 1);
         __syncthreads();
+        // group 3's MFMAs use registers only: issued after the barrier, they
+        // keep the MFMA pipe busy while the next step's first fragments load
         read_frags(nxt, 0, fa[0], fb[0]);
+        if constexpr (SCHED) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) Mma<T>::run(acc[i][j], fa[1][i], fb[1][j]);
+        if constexpr (SCHED) __builtin_amdgcn_sched_barrier(0);
     };
     if constexpr (PF == 2) {
         for (int kt = 0; kt < nk; kt += 2) {
