@@ -276,6 +276,12 @@ def time_ops(steps: int = 20) -> dict:
     vw = ox.Tensor.from_numpy(np.zeros((4096, 16384), np.float32), dev)
     cases["sgd momentum, bf16 param [4096,16384], f32 grad"] = (
         lambda: be.sgd_step(pw, gw, vw, 1e-3, 0.9, 0.0, False, stream=s), 4096 * 16384 * (2 + 4 + 4 + 2 + 4))
+    # a practical ceiling for the read + write kernels above: a plain device
+    # copy of the same 256 MiB by the vendor runtime (torch, black box)
+    tsrc = torch.empty(n * n, dtype=torch.float32, device="cuda:0").normal_()
+    tdst = torch.empty_like(tsrc)
+    cases["reference: torch device copy of 256 MiB (vendor runtime, not this backend)"] = (
+        lambda: tdst.copy_(tsrc), 2 * n * n * 4)
     out = {}
     with torch.cuda.stream(ts):
         for name, (fn, nbytes) in cases.items():

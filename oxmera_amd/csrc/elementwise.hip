@@ -180,15 +180,35 @@ __device__ __forceinline__ void st16(void *p, int64_t i, const float (&v)[DT == 
     *(uint4 *)((char *)p + i * (DT == kDtF32 ? 4 : 2)) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// n is a multiple of the vector width; every pointer 16-byte aligned.
+// st16 with a non-temporal store.
+template <int DT>
+__device__ __forceinline__ void st16_nt(void *p, int64_t i, const float (&v)[DT == kDtF32 ? 4 : 8]) {
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    uint32_t w[4];
+    if constexpr (DT == kDtF32) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = __float_as_uint(v[e]);
+    } else {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t lo = DT == kDtBF16 ? f32_to_bf16_bits(v[2 * d]) : f32_to_f16_bits(v[2 * d]);
+            const uint32_t hi = DT == kDtBF16 ? f32_to_bf16_bits(v[2 * d + 1]) : f32_to_f16_bits(v[2 * d + 1]);
+            w[d] = lo | (hi << 16);
+        }
+    }
+    __builtin_nontemporal_store(u32x4v{w[0], w[1], w[2], w[3]}, (u32x4v *)((char *)p + i * (DT == kDtF32 ? 4 : 2)));
+}
+
+// n is a multiple of the vector width; every pointer 16-byte aligned.  Each
+// thread takes two vectors a grid apart per iteration (both loads of each
+// operand in flight together); stores are non-temporal (the output is not
+// read again by this kernel).
 template <int DT, int NOPS, int OP>
 __global__ void __launch_bounds__(256) ew_contig16(int64_t n, void *out, const void *x, const void *y) {
     constexpr int V = DT == kDtF32 ? 4 : 8;
     const int64_t nv = n / V;
-    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < nv; j += (int64_t)gridDim.x * blockDim.x) {
-        float a[V], b[V];
-        ld16<DT>(x, j * V, a);
-        if constexpr (NOPS == 2) ld16<DT>(y, j * V, b);
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    auto one = [&](int64_t j, float (&a)[V], const float (&b)[V]) {
 #pragma unroll
         for (int e = 0; e < V; ++e) {
             if constexpr (NOPS == 1)
@@ -196,7 +216,25 @@ __global__ void __launch_bounds__(256) ew_contig16(int64_t n, void *out, const v
             else
                 a[e] = apply_binary<OP, float>(a[e], b[e]);
         }
-        st16<DT>(out, j * V, a);
+        st16_nt<DT>(out, j * V, a);
+    };
+    int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; j + stride < nv; j += 2 * stride) {
+        float a0[V], b0[V], a1[V], b1[V];
+        ld16<DT>(x, j * V, a0);
+        ld16<DT>(x, (j + stride) * V, a1);
+        if constexpr (NOPS == 2) {
+            ld16<DT>(y, j * V, b0);
+            ld16<DT>(y, (j + stride) * V, b1);
+        }
+        one(j, a0, b0);
+        one(j + stride, a1, b1);
+    }
+    if (j < nv) {
+        float a[V], b[V];
+        ld16<DT>(x, j * V, a);
+        if constexpr (NOPS == 2) ld16<DT>(y, j * V, b);
+        one(j, a, b);
     }
 }
 
