@@ -304,6 +304,36 @@ def test_bias_gelu_epilogue(hip, monkeypatch, dtype, out, cfg):
     assert_close(to_f32(c), widen(ref), tol, "gelu output")
 
 
+def test_gelu_accuracy(hip):
+    """The epilogue's GELU and GELU' (Abramowitz & Stegun 7.1.26 normal CDF)
+    against float64 erf on a dense grid: a K = 1 f32 GEMM with B = 1 passes
+    x through exactly, so C = GELU(x), and with A = B = 1 and aux = x,
+    C = GELU'(x).  The method's erf error is <= 1.5e-7; the bound allows
+    that plus f32 rounding and the hardware exp/rcp (1 ulp each)."""
+    from scipy.special import erf
+    d = ox.Device.rocm(0)
+    x = np.concatenate([np.linspace(-12, 12, 24001), [0.0, -0.0, 1e-30, -1e-30, 1e-5, -1e-5, 30.0, -30.0, 1e4,
+                                                         -1e4]]).astype(np.float32)
+    m, n = x.size, 64
+    xd = x.astype(np.float64)
+    phi = 0.5 * (1.0 + erf(xd / np.sqrt(2.0)))
+    g_ref = xd * phi
+    dg_ref = phi + xd * np.exp(-0.5 * xd * xd) / np.sqrt(2.0 * np.pi)
+    ones_b = ox.Tensor.from_numpy(np.ones((1, n), np.float32), d)
+    g = hip.matmul(ox.Tensor.from_numpy(x.reshape(m, 1), d), ones_b, act=ox.ACT_GELU).to_numpy()
+    z = ox.Tensor.from_numpy(np.repeat(x.reshape(m, 1), n, axis=1), d)
+    dg = hip.matmul(ox.Tensor.from_numpy(np.ones((m, 1), np.float32), d), ones_b, act=ox.ACT_DGELU,
+                    aux=z).to_numpy()
+    bound = 1e-6 * np.maximum(1.0, np.abs(xd))
+    for got, ref, what in ((g, g_ref, "GELU"), (dg, dg_ref, "GELU'")):
+        err = np.abs(got.astype(np.float64) - ref[:, None])
+        worst = int(np.argmax(err.max(axis=1) / bound))
+        assert np.all(err <= bound[:, None]), f"{what}({x[worst]}) = {got[worst, 0]} vs {ref[worst]}"
+    nan = hip.matmul(ox.Tensor.from_numpy(np.full((1, 1), np.nan, np.float32), d),
+                     ox.Tensor.from_numpy(np.ones((1, 1), np.float32), d), act=ox.ACT_GELU).to_numpy()
+    assert np.isnan(nan).all()
+
+
 @pytest.mark.parametrize("cfg", EPI_CFGS, ids=["auto", "cfg1", "cfg6"])
 @pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
 def test_dgelu_epilogue(hip, monkeypatch, dtype, cfg):
