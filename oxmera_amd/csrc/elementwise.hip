@@ -829,15 +829,30 @@ hipError_t red_launch(const RedGeom &g, const void *x, void *out, hipStream_t st
     if (g.n_out == 0) return hipSuccess;
     const bool rows = g.nr == 1 && g.rst[0] == 1 && g.n_red >= 256;
     const bool cols = !rows && g.kst[g.nk - 1] == 1 && g.n_out >= 64 && g.n_red >= 2 * kRedU;
+    // column schedule with 16-byte loads: every V-group of consecutive
+    // outputs starts 16-byte aligned at every reduced element (x aligned, the
+    // innermost kept dim a multiple of V long, every other stride a multiple
+    // of V)
+    bool cols_vec = false;
+    if constexpr (DT != kDtF64) {
+        constexpr int V = DT == kDtF32 ? 4 : 8;
+        cols_vec = cols && (uintptr_t)x % 16 == 0 && g.kshape[g.nk - 1] % V == 0;
+        for (int d = 0; d + 1 < g.nk; ++d) cols_vec = cols_vec && g.kst[d] % V == 0;
+        for (int d = 0; d < g.nr; ++d) cols_vec = cols_vec && g.rst[d] % V == 0;
+    }
     int64_t splits = 1;
     if (rows) {
-        splits = 2048 / g.n_out;
+        splits = 2048 / g.n_out;  // (8192 blocks for one output measured slower: 0.057 vs 0.051 ms)
         const int64_t cap = g.n_red / 4096;  // >= 4096 elements per block
         if (splits > cap) splits = cap;
     } else if (cols) {
-        const int64_t col_blocks = (g.n_out + 255) / 256;
+        // ~2048 blocks of 256 threads: a streaming pass needs the waves (the
+        // [8192, 8192] f32 column sum ran 58 % of HBM peak with 512 blocks,
+        // 63-65 % with 2048)
+        const int64_t per_block = cols_vec ? 256 * (DT == kDtF32 ? 4 : 8) : 256;
+        const int64_t col_blocks = (g.n_out + per_block - 1) / per_block;
         splits = 2048 / col_blocks;
-        const int64_t cap = g.n_red / 64;  // >= 64 reduced elements per thread
+        const int64_t cap = g.n_red / 32;  // >= 32 reduced elements per thread
         if (splits > cap) splits = cap;
     } else {
         hipLaunchKernelGGL((reduce_per_thread<DT, OP>), dim3(grid_for(g.n_out)), dim3(256), 0, st, g, x, out);
@@ -870,21 +885,14 @@ hipError_t red_launch(const RedGeom &g, const void *x, void *out, hipStream_t st
                                out, ws, (int)splits);
         if (splits > 1) finish(splits, (int64_t)1);
     } else {
-        bool vec = false;
         if constexpr (DT != kDtF64) {
-            // every V-group of consecutive outputs starts 16-byte aligned at
-            // every reduced element: x aligned, the innermost kept dim a
-            // multiple of V long, every other stride a multiple of V
             constexpr int V = DT == kDtF32 ? 4 : 8;
-            vec = (uintptr_t)x % 16 == 0 && g.kshape[g.nk - 1] % V == 0;
-            for (int d = 0; d + 1 < g.nk; ++d) vec = vec && g.kst[d] % V == 0;
-            for (int d = 0; d < g.nr; ++d) vec = vec && g.rst[d] % V == 0;
-            if (vec)
+            if (cols_vec)
                 hipLaunchKernelGGL((reduce_cols_vec<DT, OP>),
                                    dim3((unsigned)((g.n_out / V + 255) / 256), (unsigned)splits), dim3(256), 0, st, g,
                                    x, out, (float *)ws, (int)splits);
         }
-        if (!vec)
+        if (!cols_vec)
             hipLaunchKernelGGL((reduce_cols<DT, OP>), dim3((unsigned)((g.n_out + 255) / 256), (unsigned)splits),
                                dim3(256), 0, st, g, x, out, ws, (int)splits);
         if (splits > 1)
