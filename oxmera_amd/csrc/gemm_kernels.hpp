@@ -1222,6 +1222,9 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dl(GemmArgs
     constexpr int kStageA = BM * BKS * 2, kStageB = BN * BKS * 2;
     constexpr int kStage = kStageA + kStageB;
     constexpr int kG = BKS / 16;
+    constexpr int kQ = TM * TN;                                       // MFMAs per fragment group
+    constexpr int kReads = TM * (AMN ? 2 : 1) + TN * (BMN ? 2 : 1);  // LDS reads per fragment group
+    constexpr int kPer = (kReads + kQ / 2 - 1) / (kQ / 2);            // reads after each early MFMA
     static_assert(Elem<T>::kBytes == 2, "direct-to-LDS path is for 16-bit operands");
     static_assert(NS >= 2, "at least two stages");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
@@ -1293,6 +1296,17 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dl(GemmArgs
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j) Mma<T>::run(acc[i][j], fa[g & 1][i], fb[g & 1][j]);
+            // Group g+1's fragment reads go out over the first half of group
+            // g's MFMAs, kPer after each, so at least half the group covers
+            // their latency (left alone, the compiler issues them after
+            // group g's next-to-last MFMA and waits one MFMA later)
+            static_for<0, kQ>([&](auto qc) {
+                constexpr int q = decltype(qc)::value;
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                constexpr int left = kReads - q * kPer;
+                constexpr int nr = q < kQ / 2 ? (left < kPer ? (left > 0 ? left : 0) : kPer) : 0;
+                if constexpr (nr > 0) __builtin_amdgcn_sched_group_barrier(0x100, nr, 0);  // LDS reads
+            });
             __builtin_amdgcn_sched_barrier(0);
         });
         // every LDS read of step kt landed; this wave's DMA of step kt+1 landed
