@@ -858,6 +858,11 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
 
     Loader<T, LA, BM, NT, PF> la(abase, p.sam, p.sak, p.M - m0, p.K, tid);
     Loader<T, LB, BN, NT, PF> lb(bbase, p.sbn, p.sbk, p.N - n0, p.K, tid);
+    // 256x256 f32: the step's global loads go out one per MFMA of group 0
+    constexpr int kLoads = decltype(la)::kVmem + decltype(lb)::kVmem;
+    constexpr bool kSpreadLoads = SCHED && NT == 512 && kBytes == 4 && LA != Ld::KR && LA != Ld::MNR &&
+                                  LB != Ld::KR && LB != Ld::MNR && decltype(la)::kVmem > 0 &&
+                                  decltype(lb)::kVmem > 0 && kLoads <= TM * TN * 4;
 
     f32x16_t acc[TM][TN];
 #pragma unroll
@@ -917,7 +922,7 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
         constexpr int kLoadSet = PF == 2 ? S : 0, kStoreSet = PF == 2 ? (S ^ 1) : 0;
         la.template prefetch<kLoadSet>(kt + PF);
         lb.template prefetch<kLoadSet>(kt + PF);
-        if constexpr (SCHED) __builtin_amdgcn_sched_barrier(0);
+        if constexpr (SCHED && !kSpreadLoads) __builtin_amdgcn_sched_barrier(0);
         static_for<0, 3>([&](auto gc) {
             constexpr int g = decltype(gc)::value;
             read_frags(stage, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
@@ -925,6 +930,12 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j) Mma<T>::run(acc[i][j], fa[g & 1][i], fb[g & 1][j]);
+            if constexpr (kSpreadLoads && g == 0) {
+                static_for<0, kLoads>([&](auto) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
+                });
+            }
             if constexpr (SCHED) __builtin_amdgcn_sched_barrier(0);
         });
         la.template store<kStoreSet>(nxt, tid, kt + 1);
