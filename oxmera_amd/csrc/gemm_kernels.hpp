@@ -860,7 +860,7 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
     Loader<T, LB, BN, NT, PF> lb(bbase, p.sbn, p.sbk, p.N - n0, p.K, tid);
     // 256x256 f32: the step's global loads go out one per MFMA of group 0
     constexpr int kLoads = decltype(la)::kVmem + decltype(lb)::kVmem;
-    constexpr bool kSpreadLoads = SCHED && NT == 512 && kBytes == 4 && LA != Ld::KR && LA != Ld::MNR &&
+    constexpr bool kSpreadLoads = SCHED && NT >= 256 && kBytes == 4 && LA != Ld::KR && LA != Ld::MNR &&
                                   LB != Ld::KR && LB != Ld::MNR && decltype(la)::kVmem > 0 &&
                                   decltype(lb)::kVmem > 0 && kLoads <= TM * TN * 4;
 
