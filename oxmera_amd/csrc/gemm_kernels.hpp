@@ -858,8 +858,12 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
 
     Loader<T, LA, BM, NT, PF> la(abase, p.sam, p.sak, p.M - m0, p.K, tid);
     Loader<T, LB, BN, NT, PF> lb(bbase, p.sbn, p.sbk, p.N - n0, p.K, tid);
-    // 256x256 f32: the step's global loads go out one per MFMA of group 0
+    // f32: the step's global loads go out spread over group 0's MFMAs, one
+    // every kLoadGap (4096^3 on 256x256 tiles: 1.015 ms back to back, 1.002
+    // one per MFMA, 0.988 one every 4 MFMAs)
     constexpr int kLoads = decltype(la)::kVmem + decltype(lb)::kVmem;
+    constexpr int kLoadGapMax = kLoads > 0 ? TM * TN * 4 / kLoads : 1;
+    constexpr int kLoadGap = kLoadGapMax < 1 ? 1 : (kLoadGapMax > 4 ? 4 : kLoadGapMax);
     constexpr bool kSpreadLoads = SCHED && NT >= 256 && kBytes == 4 && LA != Ld::KR && LA != Ld::MNR &&
                                   LB != Ld::KR && LB != Ld::MNR && decltype(la)::kVmem > 0 &&
                                   decltype(lb)::kVmem > 0 && kLoads <= TM * TN * 4;
@@ -932,8 +936,8 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
                 for (int j = 0; j < TN; ++j) Mma<T>::run(acc[i][j], fa[g & 1][i], fb[g & 1][j]);
             if constexpr (kSpreadLoads && g == 0) {
                 static_for<0, kLoads>([&](auto) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
+                    __builtin_amdgcn_sched_group_barrier(0x008, kLoadGap, 0);  // kLoadGap MFMAs
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);         // one global load
                 });
             }
             if constexpr (SCHED) __builtin_amdgcn_sched_barrier(0);
