@@ -864,8 +864,7 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p)
     constexpr int kLoads = decltype(la)::kVmem + decltype(lb)::kVmem;
     constexpr int kLoadGapMax = kLoads > 0 ? TM * TN * 4 / kLoads : 1;
     constexpr int kLoadGap = kLoadGapMax < 1 ? 1 : (kLoadGapMax > 4 ? 4 : kLoadGapMax);
-    constexpr bool kSpreadLoads = SCHED && NT >= 256 && kBytes == 4 && LA != Ld::KR && LA != Ld::MNR &&
-                                  LB != Ld::KR && LB != Ld::MNR && decltype(la)::kVmem > 0 &&
+    constexpr bool kSpreadLoads = SCHED && NT >= 256 && kBytes == 4 && decltype(la)::kVmem > 0 &&
                                   decltype(lb)::kVmem > 0 && kLoads <= TM * TN * 4;
 
     f32x16_t acc[TM][TN];
