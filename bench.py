@@ -86,6 +86,18 @@ def make_inputs(kind: str):
                             "(BASELINE configs[2])",
                 "M": m, "N": n, "K": k, "batch": 1, "a_strides": [k, 1], "b_strides": [1, k], "seed": 54321}
         oshape = (m, n)
+    elif kind == "f16":
+        m = k = n = 8192
+        rng = _rng(54322)
+        a_h = rng.normal(0, 0.02, (m, k)).astype(np.float16)
+        bbuf = rng.normal(0, 0.02, (n, k)).astype(np.float16)
+        a = ox.Tensor.from_numpy(a_h, dev, ox.DType.F16)
+        b = ox.Tensor.from_numpy(bbuf, dev, ox.DType.F16).permute([1, 0])  # [K, N], strides [1, K]
+        host = ((a_h, O.F16, (m, k), (k, 1)), (bbuf, O.F16, (k, n), (1, k)))
+        desc = {"workload": "f16-in f32-out matmul 8192^3, A row-major, B transposed view strides [1,8192] "
+                            "(configs[2]'s shape and layout in f16)",
+                "M": m, "N": n, "K": k, "batch": 1, "a_strides": [k, 1], "b_strides": [1, k], "seed": 54322}
+        oshape = (m, n)
     elif kind == "c4":
         bt, m, k, n = 32, 512, 1024, 768
         rng = _rng(4444)
@@ -197,6 +209,55 @@ def time_mlp(steps: int, warmup: int):
             "ms_per_step": round(dt * 1e3, 3), "value": round(flops / dt / 1e12, 1), "unit": "TFLOP/s (6 GEMMs)",
             "pct_of_peak": round(100 * flops / dt / 1e12 / PEAK["bf16"], 2),
             "loss": float(loss.t.to_numpy()[0])}
+
+
+def mlp_cpu_baseline(rows: int = 32) -> dict:
+    """configs[4]'s six GEMMs timed with the naive oracle on the host, each on
+    `rows` seeded output rows with the operand layouts the GPU step uses
+    (transposed operands read through their strides), per-row rates summed
+    into an extrapolated time per training step.  The oracle's work does not
+    depend on the values, so the operands are synthetic bf16 (a tiled random
+    N(0, 0.02) block) of the step's shapes."""
+    from oracle import oracle as O
+    threads = min(os.cpu_count() or 1, CPU_THREADS)
+    n, d, h = 8192, 4096, 16384
+    block = O.bf16_round(np.random.default_rng(99).normal(0, 0.02, 1 << 22).astype(np.float32))
+    mats = {}
+
+    def mat(name, r, c):
+        if name not in mats:
+            mats[name] = np.resize(block, r * c)
+        return mats[name]
+
+    def view(name, r, c, transposed=False):
+        # logical [r, c]; transposed: a view of a row-major [c, r] buffer
+        buf = mat(name, c, r) if transposed else mat(name, r, c)
+        return O.StridedView(buf, O.BF16, (r, c), (1, r) if transposed else (c, 1))
+
+    gemms = [  # (name, A view, B view, output rows, K, N)
+        ("Z1 = X.W1 (+b1, GELU)", view("X", n, d), view("W1", d, h), n, d, h),
+        ("Y = H.W2 (+b2)", view("H", n, h), view("W2", h, d), n, h, d),
+        ("dW2 = H^T.dY", view("H", h, n, True), view("dY", n, d), h, n, d),
+        ("dZ1 = dY.W2^T * GELU'", view("dY", n, d), view("W2", d, h, True), n, d, h),
+        ("dW1 = X^T.dZ1", view("X", d, n, True), view("dZ1", n, h), d, n, h),
+        ("dX = dZ1.W1^T", view("dZ1", n, h), view("W1", h, d, True), n, h, d),
+    ]
+    per, total = [], 0.0
+    for name, av, bv, m, k, nn in gemms:
+        sel = np.sort(np.random.default_rng(5).choice(m, size=rows, replace=False)).astype(np.int64)
+        t0 = time.perf_counter()
+        O.matmul(av, bv, rows=sel, nthreads=threads)
+        dt = time.perf_counter() - t0
+        full = dt * m / rows
+        total += full
+        per.append({"gemm": name, "rows": rows, "of_rows": m, "s": round(dt, 3), "extrapolated_full_s": round(full, 1)})
+    flops = 6 * 2.0 * n * d * h
+    return {"value": round(flops / total / 1e12, 6), "unit": "TFLOP/s (6 GEMMs)", "cores": threads, "kind": "port",
+            "extrapolated_step_s": round(total, 1), "extrapolated": True, "per_gemm": per,
+            "sample": f"{rows} seeded output rows of each of the step's six GEMMs (synthetic bf16 operands in the "
+                      f"GPU step's layouts) by the naive oracle (oracle/oxm_oracle.c, f32 ascending-k, strided "
+                      f"reads, threaded over rows); the step time is extrapolated from the per-row rates",
+            "host_cpu": host_cpu(), "host_threads": os.cpu_count()}
 
 
 def time_vendor(kind: str, steps: int, warmup: int) -> dict:
@@ -317,33 +378,59 @@ def _views(host):
     return (O.StridedView(ab.reshape(-1), adt, ash, ast, 0), O.StridedView(bb.reshape(-1), bdt, bsh, bst, 0))
 
 
-def cpu_baseline(kind: str, host, desc, budget_s: float = 30.0):
-    """The naive oracle (oracle/oxm_oracle.c, one output row per task) on
-    the host cores: the whole output when that fits the budget, otherwise
-    a bounded random sample of output rows, extrapolated and labelled so."""
+CPU_THREADS = 16  # the GPU box's CPU share for one GPU, whatever cpu_count() reports there
+
+
+def cpu_baseline(kind: str, host, desc, budget_s: float = 30.0, rows: int | None = None):
+    """The naive oracle (oracle/oxm_oracle.c: three loops, f32 ascending-k,
+    reading through the operands' own strides; one output row per task) on
+    CPU_THREADS host threads.  rows=None: the whole output when it fits the
+    budget, else a bounded random sample grown until it takes ~budget/8;
+    rows=n: exactly n seeded rows.  A sample reports its per-row rate and the
+    full time extrapolated from it, labelled so.  Returns (line, (rows, result))
+    so that the same run also serves as the parity reference."""
     from oracle import oracle as O
-    threads = min(os.cpu_count() or 1, 16)
+    threads = min(os.cpu_count() or 1, CPU_THREADS)
     av, bv = _views(host)
     rows_total = desc["batch"] * desc["M"]
     N, K = desc["N"], desc["K"]
-    rows = threads
-    while True:
-        sel = np.sort(np.random.default_rng(7).choice(rows_total, size=rows, replace=False)).astype(np.int64)
+    rng = np.random.default_rng(7)
+    if rows is not None:
+        n = min(rows, rows_total)
+        sel = np.arange(rows_total, dtype=np.int64) if n == rows_total else \
+            np.sort(rng.choice(rows_total, size=n, replace=False)).astype(np.int64)
         t0 = time.perf_counter()
         res = O.matmul(av, bv, rows=sel, nthreads=threads)
         dt = time.perf_counter() - t0
-        if rows >= rows_total or dt >= budget_s / 8:
-            break
-        est_full = dt * rows_total / rows
-        rows = rows_total if est_full <= budget_s * 0.6 else min(rows_total, rows * max(2, int(budget_s / 8 / max(dt, 1e-3))))
-    tflops = 2.0 * rows * N * K / dt / 1e12
-    full = rows == rows_total
-    what = (f"all {rows_total} output rows" if full else
-            f"{rows} of {rows_total} output rows, extrapolated full time {dt * rows_total / rows:.1f} s")
-    return {"value": tflops, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{what} ({rows * N} outputs, K={K}) in {dt:.2f} s by the naive oxmera-cpu-style oracle "
-                      f"(oracle/oxm_oracle.c, -O2, f32 ascending-k, threaded over rows)",
-            "host_cpu": host_cpu(), "host_threads": os.cpu_count()}, (sel, res)
+    else:
+        n = threads
+        while True:
+            sel = np.sort(rng.choice(rows_total, size=n, replace=False)).astype(np.int64) if n < rows_total else \
+                np.arange(rows_total, dtype=np.int64)
+            t0 = time.perf_counter()
+            res = O.matmul(av, bv, rows=sel, nthreads=threads)
+            dt = time.perf_counter() - t0
+            if n >= rows_total or dt >= budget_s / 8:
+                break
+            est_full = dt * rows_total / n
+            n = rows_total if est_full <= budget_s * 0.6 else min(rows_total, n * max(2, int(budget_s / 8 / max(dt, 1e-3))))
+    tflops = 2.0 * n * N * K / dt / 1e12
+    full = n == rows_total
+    line = {"value": round(tflops, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "host_cpu": host_cpu(), "host_threads": os.cpu_count()}
+    if full:
+        line["sample"] = (f"all {rows_total} output rows ({n * N} outputs, K={K}): full wall time {dt:.2f} s "
+                          f"by the naive oxmera-cpu-style oracle (oracle/oxm_oracle.c, -O2, f32 ascending-k, "
+                          f"strided reads, threaded over rows)")
+        line["full_s"] = round(dt, 3)
+    else:
+        line["sample"] = (f"{n} seeded rows of {rows_total} ({n * N} outputs, K={K}) in {dt:.2f} s by the naive "
+                          f"oxmera-cpu-style oracle (oracle/oxm_oracle.c, -O2, f32 ascending-k, strided reads, "
+                          f"threaded over rows)")
+        line["s_per_row"] = dt / n
+        line["extrapolated_full_s"] = round(dt * rows_total / n, 1)
+        line["extrapolated"] = True
+    return line, (sel, res)
 
 
 def _abs_product(host, sel, desc):
@@ -379,7 +466,7 @@ def spot_check(kind: str, res, sample, host=None, comp_rows: int = 64):
     got = out[sel].astype(np.float64)
     ref = ref.astype(np.float64)
     rms = float(np.sqrt(np.mean(ref * ref))) or 1e-30
-    tol = 1e-5 * np.sqrt(res["desc"]["K"]) if kind != "bf16" else 1e-2
+    tol = 1e-2 if kind in ("bf16", "f16") else 1e-5 * np.sqrt(res["desc"]["K"])
     worst = float(np.max(np.abs(got - ref) / (tol * np.maximum(np.abs(ref), rms))))
     d = {"rows": int(len(sel)), "tol": float(tol), "max_err_over_tol": round(worst, 4), "pass": worst <= 1.0}
     if host is not None:
@@ -391,6 +478,8 @@ def spot_check(kind: str, res, sample, host=None, comp_rows: int = 64):
 
 
 def kernel_name(kind: str) -> str:
+    if kind == "f16":
+        return "gemm_kernel_dl<f16_t,256,256,2,4,2,64> (direct-to-LDS, 2 stages of 64 k, 8 waves)"
     if kind == "bf16":
         return "gemm_kernel_dl<bf16_t,256,256,2,4,2,64> (direct-to-LDS, 2 stages of 64 k, 8 waves)"
     if kind == "f32":
@@ -412,39 +501,61 @@ def traffic_for(kind: str):
 def roofline(kind: str, res):
     avg_ms = res["total_ms"] / res["steps"]
     achieved = res["flops"] / (avg_ms * 1e-3) / 1e12
-    peak = PEAK["bf16" if kind == "bf16" else "f32"]
+    peak = PEAK["bf16" if kind in ("bf16", "f16") else "f32"]
     return {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-            "frac": round(achieved / peak, 4), "traffic": traffic_for(kind) if kind in ("f32", "bf16") else None,
+            "frac": round(achieved / peak, 4), "traffic": traffic_for(kind),
             "kernel": kernel_name(kind), "avg_launch_ms": round(avg_ms, 4)}
 
 
+# Rows of the oracle run (CPU baseline and parity reference at once) per
+# configuration: None = every output row; n = n seeded rows (the per-row
+# rate is then extrapolated to the full output).
+ORACLE_ROWS = {"f32": None, "c1": None, "c2odd": None, "c4": None, "bf16": 256, "f16": 64}
+
+
 def extra_line(kind: str, steps: int, warmup: int) -> dict:
-    """Timing plus an oracle parity check for one more configuration: the
-    whole output for C1 and C4, 64 sampled rows otherwise."""
-    from oracle import oracle as O
+    """Timing plus the oracle run for one more configuration: its CPU
+    baseline and the parity check of the timed output against it (the whole
+    output for C1, C2-odd and C4; 256 seeded rows x every column for C3)."""
     steps = max(10, steps // 2) if kind not in ("c1",) else max(50, steps)
     r = time_gpu(kind, steps, warmup)
     r["steps"] = steps
     d = r["desc"]
     v = r["flops"] * steps / (r["total_ms"] * 1e-3) / 1e12
     rows_total = d["batch"] * d["M"]
-    if kind in ("c1", "c4"):
-        sel = np.arange(rows_total, dtype=np.int64)
-    else:
-        sel = np.sort(np.random.default_rng(11).choice(rows_total, size=64, replace=False)).astype(np.int64)
-    av, bv = _views(r["host"])
-    ref = O.matmul(av, bv, rows=sel, nthreads=min(os.cpu_count() or 1, 16))
-    peak = PEAK["bf16" if kind == "bf16" else "f32"]
+    nrows = ORACLE_ROWS[kind]
+    cb, sample = cpu_baseline(kind, r["host"], d, rows=rows_total if nrows is None else nrows)
+    peak = PEAK["f32" if kind in ("f32", "c1", "c2odd", "c4") else "bf16"]
     line = {"config": d, "value": round(v, 2), "unit": "TFLOP/s", "pct_of_peak": round(100 * v / peak, 2),
             "ms_per_step": round(r["total_ms"] / steps, 4),
             "median_launch_ms": round(r["per_ms"][len(r["per_ms"]) // 2], 4),
-            "parity_spot_check": spot_check(kind, r, (sel, ref), r["host"])}
+            "parity_spot_check": spot_check(kind, r, sample, r["host"]), "cpu_baseline": cb}
     if kind == "c1":
         line["us_per_launch"] = round(1e3 * r["total_ms"] / steps, 2)
         line["note"] = "launch-latency bound (0.2 us of MFMA work at peak); no roofline target"
-    if kind in ("bf16", "f32"):
+    if kind in ("bf16", "f32", "f16"):
         line["roofline"] = roofline(kind, r)
     return line
+
+
+def summarize_trace(path: str, kernel: str, timed: int, after: int) -> dict:
+    """Durations of the launches bench.py timed, from a rocprofv3 kernel trace
+    of the same command: the dispatches of the kernel (name containing
+    `kernel`) in dispatch order, minus the `after` individually timed ones at
+    the end, last `timed` of the rest.  Their average is what the HIP-event
+    figure (ms_per_step) measures, without the warm-up launches."""
+    import csv
+    rows = [r for r in csv.DictReader(open(path)) if kernel in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    if len(rows) < timed + after:
+        raise SystemExit(f"{len(rows)} dispatches of {kernel!r}, fewer than {timed} + {after}")
+    win = rows[len(rows) - after - timed:len(rows) - after]
+    d = np.array([int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in win], dtype=np.float64) / 1e6
+    names = sorted({r["Kernel_Name"] for r in win})
+    return {"kernel": names, "dispatches_total": len(rows), "window": [len(rows) - after - timed, len(rows) - after],
+            "avg_ms": round(float(d.mean()), 5), "median_ms": round(float(np.median(d)), 5),
+            "min_ms": round(float(d.min()), 5), "max_ms": round(float(d.max()), 5),
+            "span_ms": round((int(win[-1]["End_Timestamp"]) - int(win[0]["Start_Timestamp"])) / 1e6 / timed, 5)}
 
 
 def main():
@@ -452,9 +563,15 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=["f32", "bf16", "mlp", "ops", "c1", "c2odd", "c4"], default="f32",
-                    help="f32 / bf16 (the headline configurations) or c1 / c2odd / c4 time one GEMM; mlp times "
-                         "the MLP step alone (for profiling)")
+    ap.add_argument("--workload", choices=["f32", "bf16", "f16", "mlp", "ops", "c1", "c2odd", "c4"], default="f32",
+                    help="f32 / bf16 (the headline configurations) or f16 / c1 / c2odd / c4 time one GEMM; mlp "
+                         "times the MLP step alone (for profiling)")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="summarize a rocprofv3 kernel_trace.csv of a bench run instead of running: the timed "
+                         "window (--timed launches of --kernel, followed by --after per-launch timings)")
+    ap.add_argument("--kernel", default="gemm_kernel", help="substring of the kernel name (--summarize-trace)")
+    ap.add_argument("--timed", type=int, default=50, help="launches in the timed window (--summarize-trace)")
+    ap.add_argument("--after", type=int, default=20, help="launches after the timed window (--summarize-trace)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the extra workload")
     ap.add_argument("--vendor", action="store_true",
                     help="time torch.matmul (the vendor library, hipBLASLt, run as a black box) on the same "
@@ -463,6 +580,9 @@ def main():
                     help="run only a plain 256 MiB device copy (10x), the reference for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE scaling")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(json.dumps(summarize_trace(args.summarize_trace, args.kernel, args.timed, args.after)), flush=True)
+        return
     if args.copy_calibration:
         import torch
         src = torch.empty(64 << 20, dtype=torch.float32, device="cuda:0").normal_()
@@ -502,23 +622,26 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if main_kind == "bf16" else "f32",
+        "dtype": main_kind if main_kind in ("bf16", "f16") else "f32",
         "data": "synthetic",
         "config": res["desc"],
-        "pct_of_peak": round(100 * value / PEAK["bf16" if main_kind == "bf16" else "f32"], 2),
+        "pct_of_peak": round(100 * value / PEAK["bf16" if main_kind in ("bf16", "f16") else "f32"], 2),
         "median_launch_ms": round(res["per_ms"][len(res["per_ms"]) // 2], 4),
         "roofline": roofline(main_kind, res),
     }
     if not args.no_cpu:
-        cb, sample = cpu_baseline(main_kind, res["host"], res["desc"])
+        nrows = ORACLE_ROWS.get(main_kind)
+        rows_total = res["desc"]["batch"] * res["desc"]["M"]
+        cb, sample = cpu_baseline(main_kind, res["host"], res["desc"], rows=rows_total if nrows is None else nrows)
         line["cpu_baseline"] = cb
         line["parity_spot_check"] = spot_check(main_kind, res, sample, res["host"])
         del res
         line["extra"] = {}
-        others = [k for k in ("bf16", "f32") if k != main_kind] + ["c1", "c2odd", "c4"]
+        others = [k for k in ("bf16", "f32") if k != main_kind] + ["f16", "c1", "c2odd", "c4"]
         for other in others:
             line["extra"][other] = extra_line(other, args.steps, args.warmup)
         line["extra"]["mlp"] = time_mlp(max(3, args.steps // 10), 2)
+        line["extra"]["mlp"]["cpu_baseline"] = mlp_cpu_baseline()
         line["extra"]["ops"] = time_ops()
     print(json.dumps(line), flush=True)
 

@@ -16,7 +16,14 @@
  *  - Status codes map 1:1 onto oxmera_core::Error variants
  *    (crates/oxmera-core/src/error.rs:14-102); oxm_last_error() returns a
  *    thread-local message naming the operation and its operands.
- *  - Validation runs completely before any device work is launched.
+ *  - Validation runs completely before any device work is launched.  A view
+ *    whose element count or byte range would overflow int64 is
+ *    OXM_E_INDEX_OUT_OF_BOUNDS.  An output that shares memory with an input
+ *    (or with another output of the same call) is OXM_E_INVALID_ARGUMENT:
+ *    outputs are fresh storage (crates/oxmera-ops/src/lib.rs:16-17).  The
+ *    one exception is an elementwise input that IS the output element for
+ *    element (same first element and strides), which unary and binary ops
+ *    accept (in-place update).
  *  - stream == NULL: the call is synchronous (the result may be read as soon
  *    as it returns, as MatmulOps::matmul returns a value).  A non-NULL
  *    hipStream_t makes it asynchronous on that stream.
@@ -117,6 +124,14 @@ oxm_status oxm_device_count(int32_t *count);
 
 /* Backend::name() (crates/oxmera-runtime/src/lib.rs:33). */
 const char *oxm_backend_name(void);
+
+/* The bytes a view can address, relative to v->data: [*lo_bytes, *hi_bytes)
+ * (both 0 for an empty view).  Tensor::from_storage's rule
+ * (crates/oxmera-tensor/src/tensor.rs:21-28) needs exactly this range to lie
+ * inside the storage; every product and sum is overflow-checked, and a range
+ * that does not fit int64 is OXM_E_INDEX_OUT_OF_BOUNDS.  Host-only: it
+ * touches no device and needs no GPU. */
+oxm_status oxm_view_byte_range(const oxm_view *v, int64_t *lo_bytes, int64_t *hi_bytes);
 
 /* broadcast_shapes (crates/oxmera-core/src/shape.rs:45-58): NumPy rules; on
  * refusal OXM_E_BROADCAST_INCOMPATIBLE and the message carries both operands
@@ -237,8 +252,12 @@ oxm_status oxm_sgd_step(const oxm_view *param, const oxm_view *grad, const oxm_v
 oxm_status oxm_alloc(int32_t device, size_t bytes, void **out);
 oxm_status oxm_free(int32_t device, void *ptr);
 
-/* Byte copy between host (-1) and device (>= 0) memory; synchronous when
- * stream is NULL. */
+/* Byte copy between host (-1) and device (>= 0) memory.  stream == NULL:
+ * synchronous.  Otherwise the copy is ordered after the work already queued
+ * on `stream`; a copy to or from host memory also completes before the call
+ * returns (so the host buffer may be read or freed at once), a device-to-
+ * device copy stays asynchronous.  Overlapping device ranges are
+ * OXM_E_INVALID_ARGUMENT. */
 oxm_status oxm_copy(void *dst, int32_t dst_device, const void *src, int32_t src_device, size_t bytes, void *stream);
 
 /* Wait for all work on the device. */

@@ -142,7 +142,8 @@ def matmul(a: StridedView, b: StridedView, *, out_dtype: int = F32, bias: np.nda
     vb, kb = b._struct()
     bias_c = np.ascontiguousarray(bias) if bias is not None else None
     aux_c = np.ascontiguousarray(aux) if aux is not None else None
-    nt = nthreads or os.cpu_count() or 1
+    # the GPU box gives one process a 16-core share whatever cpu_count() reports
+    nt = nthreads or min(os.cpu_count() or 1, 16)
     st = lib().oxm_oracle_gemm(C.byref(va), C.byref(vb), out_dtype,
                                bias_c.ctypes.data if bias_c is not None else None, bias_dtype, act,
                                aux_c.ctypes.data if aux_c is not None else None,

@@ -66,6 +66,7 @@ _PROTOS = {
     "oxm_last_error": (C.c_char_p, []),
     "oxm_backend_name": (C.c_char_p, []),
     "oxm_device_count": (C.c_int, [C.POINTER(C.c_int32)]),
+    "oxm_view_byte_range": (C.c_int, [C.POINTER(OxmView), C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
     "oxm_broadcast_shapes": (C.c_int, [C.c_int32, C.POINTER(C.c_int64), C.c_int32, C.POINTER(C.c_int64),
                                        C.POINTER(C.c_int32), C.POINTER(C.c_int64)]),
     "oxm_gemm_infer": (C.c_int, [C.POINTER(OxmView), C.POINTER(OxmView), C.POINTER(C.c_int32),

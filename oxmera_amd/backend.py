@@ -20,7 +20,8 @@ import threading
 from typing import Sequence
 
 from . import _lib
-from .core import (BackendUnavailable, Device, DType, NotImplementedOp, check)
+from .core import (BackendUnavailable, Device, DeviceMismatch, DType, DTypeMismatch, NotImplementedOp,
+                   ShapeMismatch, check)
 from .tensor import Tensor
 
 
@@ -69,8 +70,24 @@ class HipBackend:
         c = out.abi_view()
         ep = None
         if bias is not None or act != _lib.ACT_NONE or aux is not None or colsum is not None:
-            if colsum is not None and (colsum.dtype != DType.F32 or colsum.shape != (oshape[-1],)):
-                raise ValueError(f"colsum must be F32 [{oshape[-1]}], got {colsum.dtype.name} {list(colsum.shape)}")
+            # the epilogue's buffers reach the C-ABI as raw pointers: their
+            # dtype, shape, layout and device are checked here
+            n = oshape[-1]
+            for name, t, dts, shape in (("bias", bias, (DType.F32, DType.BF16, DType.F16), (n,)),
+                                        ("aux", aux, (out.dtype,), tuple(out.shape)),
+                                        ("colsum", colsum, (DType.F32,), (n,))):
+                if t is None:
+                    continue
+                if t.dtype not in dts:
+                    raise DTypeMismatch(f"dtype mismatch: expected {dts[0].name}, got {t.dtype.name} in matmul "
+                                        f"({name})")
+                if tuple(t.shape) != shape:
+                    raise ShapeMismatch(f"shape mismatch: expected {list(shape)}, got {list(t.shape)} in matmul "
+                                        f"({name})")
+                if not t.layout.is_contiguous():
+                    raise NotImplementedOp(f"matmul is not implemented for a non-contiguous {name}")
+                if t.device != lhs.device:
+                    raise DeviceMismatch(f"device mismatch: {lhs.device} vs {t.device} in matmul ({name})")
             ep = _lib.OxmEpilogue(C.c_void_p(bias.data_ptr() if bias is not None else 0),
                                   int(bias.dtype) if bias is not None else 0, int(act),
                                   C.c_void_p(aux.data_ptr() if aux is not None else 0),

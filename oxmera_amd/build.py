@@ -5,7 +5,8 @@ Each HIP / C++ translation unit under ``oxmera_amd/csrc`` is compiled with
 then linked into one shared library exporting the C-ABI of
 ``include/oxm.h``.  hipcc cross-compiles, so this runs without a GPU.
 
-Usage: ``python -m oxmera_amd.build`` (or ``__graft_entry__.build()``).
+Usage: ``python -m oxmera_amd.build`` (or ``__graft_entry__.build()``);
+``python -m oxmera_amd.build --changed`` recompiles only out-of-date units.
 """
 from __future__ import annotations
 
@@ -70,12 +71,26 @@ def build_cli(verbose: bool = True) -> Path:
     return CLI
 
 
-def build(verbose: bool = True) -> Path:
-    """Compile every translation unit and link ``liboxm.so``; returns its path."""
+def _stale(src: str) -> bool:
+    """Whether a unit's object is older than its source or any header under
+    csrc/ or include/ (a unit includes only those)."""
+    obj = BUILD / (src.replace(".", "_") + ".o")
+    if not obj.exists():
+        return True
+    t = obj.stat().st_mtime
+    deps = [CSRC / src, *CSRC.glob("*.hpp"), *(PKG.parent / "include").glob("*.h")]
+    return any(d.stat().st_mtime > t for d in deps)
+
+
+def build(verbose: bool = True, changed_only: bool = False) -> Path:
+    """Compile every translation unit (with ``changed_only``, only those whose
+    object is out of date) and link ``liboxm.so``; returns its path."""
     BUILD.mkdir(exist_ok=True)
-    jobs = min(len(SOURCES), max(1, min(os.cpu_count() or 1, 16)))
+    todo = [s for s in SOURCES if not changed_only or _stale(s)]
+    jobs = min(max(1, len(todo)), max(1, min(os.cpu_count() or 1, 16)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        list(ex.map(_compile, todo))
+    objs = [BUILD / (s.replace(".", "_") + ".o") for s in SOURCES]
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [_hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -88,6 +103,6 @@ def build(verbose: bool = True) -> Path:
 
 
 if __name__ == "__main__":
-    build()
+    build(changed_only="--changed" in sys.argv[1:])
     build_cli()
     sys.exit(0)

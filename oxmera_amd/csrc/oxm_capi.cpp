@@ -90,13 +90,74 @@ oxm_status check_view(const oxm_view *v, const char *what, const char *op) {
     for (int i = 0; i < v->ndim; ++i)
         if (v->shape[i] < 0) return fail(OXM_E_INVALID_ARGUMENT, "%s: %s has negative extent", op, what);
     if (v->offset < 0) return fail(OXM_E_INVALID_ARGUMENT, "%s: %s has negative offset", op, what);
+    // every later element count (numel, M*N, batch products) must fit int64
+    bool empty = false;
+    for (int i = 0; i < v->ndim; ++i) empty = empty || v->shape[i] == 0;
+    int64_t n = 1;
+    for (int i = 0; i < v->ndim && !empty; ++i)
+        if (__builtin_mul_overflow(n, v->shape[i], &n))
+            return fail(OXM_E_INDEX_OUT_OF_BOUNDS, "%s: %s of shape %s has more elements than int64 can count", op,
+                        what, shape_str(v->ndim, v->shape).c_str());
     return OXM_OK;
 }
 
+// Element count of a view that passed check_view (which rules out overflow).
 int64_t numel(const oxm_view *v) {
     int64_t n = 1;
     for (int i = 0; i < v->ndim; ++i) n *= v->shape[i];
     return n;
+}
+
+// The bytes a non-empty view can address, relative to v->data: [lo, hi).
+// Every product and sum is checked, so a view whose strides or offset would
+// wrap int64 (e.g. stride 2^61 of an F32 view) is refused instead of
+// producing a range that looks valid.
+bool byte_range(const oxm_view *v, int64_t *lo_bytes, int64_t *hi_bytes) {
+    const int64_t es = dtype_size(v->dtype);
+    int64_t lo = v->offset, hi = v->offset;
+    for (int i = 0; i < v->ndim; ++i) {
+        int64_t span;
+        if (__builtin_mul_overflow(v->shape[i] - 1, v->strides[i], &span)) return false;
+        if (__builtin_add_overflow(span < 0 ? lo : hi, span, span < 0 ? &lo : &hi)) return false;
+    }
+    int64_t hi1;
+    if (__builtin_add_overflow(hi, (int64_t)1, &hi1)) return false;
+    return !__builtin_mul_overflow(lo, es, lo_bytes) && !__builtin_mul_overflow(hi1, es, hi_bytes);
+}
+
+// Absolute address range [lo, hi) of a non-empty view that passed
+// check_view_memory (its byte range is known not to overflow).
+struct Span {
+    uintptr_t lo, hi;
+};
+Span span_of(const oxm_view *v) {
+    int64_t lo = 0, hi = 0;
+    if (numel(v) == 0 || !byte_range(v, &lo, &hi)) return {0, 0};
+    return {(uintptr_t)v->data + (uintptr_t)lo, (uintptr_t)v->data + (uintptr_t)hi};
+}
+Span span_bytes(const void *p, int64_t bytes) { return {(uintptr_t)p, (uintptr_t)p + (uintptr_t)bytes}; }
+bool overlaps(Span x, Span y) { return x.lo < x.hi && y.lo < y.hi && x.lo < y.hi && y.lo < x.hi; }
+
+// An output must be fresh storage ("the output of every operation is a fresh
+// contiguous tensor", crates/oxmera-ops/src/lib.rs:16-17): a kernel that
+// writes tiles, transposes through LDS or splits a reduction would read
+// values it has already overwritten.  Byte ranges are compared, so two
+// interleaved views of one buffer (even and odd columns) are refused too.
+oxm_status refuse_overlap(Span out, const char *out_name, Span in, const char *in_name, const char *op) {
+    if (!overlaps(out, in)) return OXM_OK;
+    return fail(OXM_E_INVALID_ARGUMENT, "%s: the %s overlaps the %s (an output must not share memory with an input)",
+                op, out_name, in_name);
+}
+
+// An elementwise input may be the output itself -- same first element and,
+// over the output's shape, the output's own strides -- since every element is
+// read and written by the same thread; any other overlap is refused.
+bool same_elements(const oxm_view *out, const void *in_first, const int64_t *in_strides) {
+    const int es = dtype_size(out->dtype);
+    if ((const char *)in_first != (const char *)out->data + out->offset * es) return false;
+    for (int d = 0; d < out->ndim; ++d)
+        if (out->shape[d] != 1 && in_strides[d] != out->strides[d]) return false;
+    return true;
 }
 
 bool is_contiguous(const oxm_view *v) {
@@ -144,7 +205,9 @@ oxm_status check_device_range(const void *p, int64_t lo_bytes, int64_t hi_bytes,
             return fail(OXM_E_DEVICE_MISMATCH, "%s: %s lives on %s, expected %s", op, what,
                         device_str(info.device).c_str(), device_str(device).c_str());
         const int64_t rel = (int64_t)((uintptr_t)p - rbase);
-        if (rel + lo_bytes < 0 || rel + hi_bytes > (int64_t)info.bytes)
+        int64_t a0 = 0, a1 = 0;
+        if (__builtin_add_overflow(rel, lo_bytes, &a0) || __builtin_add_overflow(rel, hi_bytes, &a1) || a0 < 0 ||
+            a1 > (int64_t)info.bytes)
             return fail(OXM_E_INDEX_OUT_OF_BOUNDS,
                         "%s: %s addresses bytes [%lld, %lld) relative to its pointer, outside its %zu-byte allocation",
                         op, what, (long long)lo_bytes, (long long)hi_bytes, info.bytes);
@@ -169,13 +232,13 @@ oxm_status check_device_range(const void *p, int64_t lo_bytes, int64_t hi_bytes,
         (void)hipGetLastError();
         return fail(OXM_E_HIP, "%s: cannot query the allocation of %s", op, what);
     }
-    const char *b = (const char *)base;
-    const char *lo = (const char *)p + lo_bytes;
-    const char *hi = (const char *)p + hi_bytes;
-    if (lo < b || hi > b + size)
+    const int64_t rel = (int64_t)((uintptr_t)p - (uintptr_t)base);
+    int64_t a0 = 0, a1 = 0;
+    if (__builtin_add_overflow(rel, lo_bytes, &a0) || __builtin_add_overflow(rel, hi_bytes, &a1) || a0 < 0 ||
+        a1 > (int64_t)size)
         return fail(OXM_E_INDEX_OUT_OF_BOUNDS,
                     "%s: %s addresses bytes [%lld, %lld) relative to its pointer, outside its %zu-byte allocation", op,
-                    what, (long long)(lo - (const char *)p), (long long)(hi - (const char *)p), size);
+                    what, (long long)lo_bytes, (long long)hi_bytes, size);
     return OXM_OK;
 }
 
@@ -183,14 +246,11 @@ oxm_status check_device_range(const void *p, int64_t lo_bytes, int64_t hi_bytes,
 // (Tensor::from_storage's rule, crates/oxmera-tensor/src/tensor.rs:21-28).
 oxm_status check_view_memory(const oxm_view *v, const char *what, const char *op) {
     if (numel(v) == 0) return OXM_OK;
-    int es = dtype_size(v->dtype);
-    int64_t lo = v->offset, hi = v->offset;
-    for (int i = 0; i < v->ndim; ++i) {
-        int64_t span = (v->shape[i] - 1) * v->strides[i];
-        if (span < 0) lo += span;
-        else hi += span;
-    }
-    return check_device_range(v->data, lo * es, (hi + 1) * es, v->device, what, op);
+    int64_t lo = 0, hi = 0;
+    if (!byte_range(v, &lo, &hi))
+        return fail(OXM_E_INDEX_OUT_OF_BOUNDS, "%s: the byte range of %s (shape %s) overflows int64", op, what,
+                    shape_str(v->ndim, v->shape).c_str());
+    return check_device_range(v->data, lo, hi, v->device, what, op);
 }
 
 struct DeviceGuard {
@@ -389,6 +449,22 @@ oxm_status oxm_device_count(int32_t *count) {
     return ok();
 }
 
+oxm_status oxm_view_byte_range(const oxm_view *v, int64_t *lo_bytes, int64_t *hi_bytes) {
+    const char *op = "view_byte_range";
+    oxm_status st;
+    if ((st = check_view(v, "view", op)) != OXM_OK) return st;
+    if (!lo_bytes || !hi_bytes) return fail(OXM_E_INVALID_ARGUMENT, "%s: NULL output pointer", op);
+    *lo_bytes = *hi_bytes = 0;
+    if (numel(v) == 0) return ok();
+    int64_t lo = 0, hi = 0;
+    if (!byte_range(v, &lo, &hi))
+        return fail(OXM_E_INDEX_OUT_OF_BOUNDS, "%s: the byte range of a view of shape %s overflows int64", op,
+                    shape_str(v->ndim, v->shape).c_str());
+    *lo_bytes = lo;
+    *hi_bytes = hi;
+    return ok();
+}
+
 oxm_status oxm_broadcast_shapes(int32_t na, const int64_t *a, int32_t nb, const int64_t *b, int32_t *nout,
                                 int64_t *out) {
     if (na < 0 || nb < 0 || na > OXM_MAX_DIMS || nb > OXM_MAX_DIMS || (na && !a) || (nb && !b) || !nout || !out)
@@ -501,6 +577,27 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
         return st;
     if (ep->colsum && (st = check_device_range(ep->colsum, 0, N * 4, a->device, "colsum", op)) != OXM_OK)
         return st;
+    {
+        const Span sa = span_of(a), sb = span_of(b), sc = span_of(c);
+        const Span sbias = ep->bias ? span_bytes(ep->bias, N * dtype_size(ep->bias_dtype)) : Span{0, 0};
+        const Span saux = ep->aux ? span_bytes(ep->aux, batch * M * N * oes) : Span{0, 0};
+        const Span scs = ep->colsum ? span_bytes(ep->colsum, N * 4) : Span{0, 0};
+        const struct {
+            Span out;
+            const char *name;
+        } outs[3] = {{sc, "output"}, {ep->act == OXM_ACT_DGELU ? Span{0, 0} : saux, "aux output"}, {scs, "colsum"}};
+        const struct {
+            Span in;
+            const char *name;
+        } ins[4] = {{sa, "lhs"}, {sb, "rhs"}, {sbias, "bias"}, {ep->act == OXM_ACT_DGELU ? saux : Span{0, 0}, "aux"}};
+        for (const auto &o : outs) {
+            for (const auto &i : ins)
+                if ((st = refuse_overlap(o.out, o.name, i.in, i.name, op)) != OXM_OK) return st;
+        }
+        if ((st = refuse_overlap(sc, "output", saux, "aux output", op)) != OXM_OK) return st;
+        if ((st = refuse_overlap(sc, "output", scs, "colsum", op)) != OXM_OK) return st;
+        if ((st = refuse_overlap(saux, "aux", scs, "colsum", op)) != OXM_OK) return st;
+    }
 
     const int es = dtype_size(a->dtype);
     oxm::GemmArgs g;
@@ -606,6 +703,7 @@ oxm_status oxm_sum_rows(const oxm_view *x, const oxm_view *out, void *stream) {
     DeviceGuard guard(x->device);
     if ((st = check_view_memory(x, "input", op)) != OXM_OK) return st;
     if ((st = check_view_memory(out, "out", op)) != OXM_OK) return st;
+    if ((st = refuse_overlap(span_of(out), "output", span_of(x), "input", op)) != OXM_OK) return st;
     int es = dtype_size(x->dtype);
     hipStream_t s = (hipStream_t)stream;
     hipError_t e = oxm::launch_sum_rows((const char *)x->data + x->offset * es, x->dtype, x->shape[0], x->shape[1],
@@ -655,6 +753,18 @@ oxm_status oxm_mse_loss_grad(const oxm_view *y, const oxm_view *t, const oxm_vie
     if ((st = check_view_memory(dy, "dy", op)) != OXM_OK) return st;
     if ((st = check_view_memory(loss, "loss", op)) != OXM_OK) return st;
     if (dy_colsum && (st = check_view_memory(dy_colsum, "dy_colsum", op)) != OXM_OK) return st;
+    {
+        const Span outs[3] = {span_of(dy), span_of(loss), dy_colsum ? span_of(dy_colsum) : Span{0, 0}};
+        const char *onames[3] = {"dy", "loss", "dy_colsum"};
+        const Span ins[2] = {span_of(y), span_of(t)};
+        const char *inames[2] = {"y", "target"};
+        for (int o = 0; o < 3; ++o) {
+            for (int i = 0; i < 2; ++i)
+                if ((st = refuse_overlap(outs[o], onames[o], ins[i], inames[i], op)) != OXM_OK) return st;
+            for (int o2 = o + 1; o2 < 3; ++o2)
+                if ((st = refuse_overlap(outs[o], onames[o], outs[o2], onames[o2], op)) != OXM_OK) return st;
+        }
+    }
     int es = dtype_size(y->dtype);
     hipStream_t s = (hipStream_t)stream;
     hipError_t e = oxm::launch_mse((const char *)y->data + y->offset * es, (const char *)t->data + t->offset * es,
@@ -723,9 +833,21 @@ oxm_status oxm_copy(void *dst, int32_t dst_device, const void *src, int32_t src_
         oxm_status st = check_device_range(src, 0, (int64_t)bytes, src_device, "src", "copy");
         if (st != OXM_OK) return st;
     }
+    if (dst_device >= 0 && src_device >= 0 &&
+        overlaps(span_bytes(dst, (int64_t)bytes), span_bytes(src, (int64_t)bytes)))
+        return fail(OXM_E_INVALID_ARGUMENT, "copy: the destination overlaps the source");
     DeviceGuard guard(dst_device >= 0 ? dst_device : (src_device >= 0 ? src_device : 0));
     hipStream_t s = (hipStream_t)stream;
-    hipError_t e = s ? hipMemcpyAsync(dst, src, bytes, kind, s) : hipMemcpy(dst, src, bytes, kind);
+    hipError_t e;
+    if (!s) {
+        e = hipMemcpy(dst, src, bytes, kind);
+    } else {
+        // ordered after the work queued on the stream; a copy to or from host
+        // memory also completes before the call returns (the host buffer may
+        // be read or released right after)
+        e = hipMemcpyAsync(dst, src, bytes, kind, s);
+        if (e == hipSuccess && kind != hipMemcpyDeviceToDevice) e = hipStreamSynchronize(s);
+    }
     if (e != hipSuccess) return hip_fail(e, "copy");
     return ok();
 }
@@ -746,6 +868,9 @@ oxm_status oxm_unary(int32_t op, const oxm_view *x, const oxm_view *out, void *s
     if ((st = check_view_memory(x, "input", name)) != OXM_OK) return st;
     if ((st = check_view_memory(out, "out", name)) != OXM_OK) return st;
     const int es = dtype_size(x->dtype);
+    if (!same_elements(out, (const char *)x->data + x->offset * es, x->strides) &&
+        (st = refuse_overlap(span_of(out), "output", span_of(x), "input", name)) != OXM_OK)
+        return st;
     std::vector<int64_t> ost(x->ndim > 0 ? x->ndim : 1);
     int64_t acc = 1;
     for (int d = x->ndim - 1; d >= 0; --d) {
@@ -802,8 +927,14 @@ oxm_status oxm_binary(int32_t op, const oxm_view *a, const oxm_view *b, const ox
         sb[d] = (db >= 0 && b->shape[db] != 1) ? b->strides[db] : 0;
     }
     const int64_t *sts[3] = {so, sa, sb};
-    oxm::EwShape sh = collapse(nd, shape, sts, 3);
     const int es = dtype_size(a->dtype);
+    if (!same_elements(out, (const char *)a->data + a->offset * es, sa) &&
+        (st = refuse_overlap(span_of(out), "output", span_of(a), "lhs", name)) != OXM_OK)
+        return st;
+    if (!same_elements(out, (const char *)b->data + b->offset * es, sb) &&
+        (st = refuse_overlap(span_of(out), "output", span_of(b), "rhs", name)) != OXM_OK)
+        return st;
+    oxm::EwShape sh = collapse(nd, shape, sts, 3);
     void *po = (char *)out->data + out->offset * es;
     const void *pa = (const char *)a->data + a->offset * es, *pb = (const char *)b->data + b->offset * es;
     const void *ptrs[3] = {po, pa, pb};
@@ -863,6 +994,7 @@ oxm_status oxm_reduce(int32_t op, const oxm_view *x, const int32_t *axes, int32_
     DeviceGuard guard(x->device);
     if ((st = check_view_memory(x, "input", name)) != OXM_OK) return st;
     if ((st = check_view_memory(out, "out", name)) != OXM_OK) return st;
+    if ((st = refuse_overlap(span_of(out), "output", span_of(x), "input", name)) != OXM_OK) return st;
     // kept and reduced dims, each collapsed where the input walks them as one
     int64_t ks[OXM_MAX_DIMS], kt[OXM_MAX_DIMS], rs[OXM_MAX_DIMS], rt[OXM_MAX_DIMS];
     int nk = 0, nr = 0;
@@ -923,9 +1055,12 @@ oxm_status oxm_copy_view(const oxm_view *src, const oxm_view *dst, void *stream)
     DeviceGuard guard(src->device);
     if ((st = check_view_memory(src, "src", op)) != OXM_OK) return st;
     if ((st = check_view_memory(dst, "dst", op)) != OXM_OK) return st;
+    const int es = dtype_size(src->dtype);
+    // dst == src element for element: nothing to move
+    if (same_elements(dst, (const char *)src->data + src->offset * es, src->strides)) return ok();
+    if ((st = refuse_overlap(span_of(dst), "destination", span_of(src), "source", op)) != OXM_OK) return st;
     const int64_t *sts[3] = {dst->strides, src->strides, nullptr};
     oxm::EwShape sh = collapse(src->ndim, src->shape, sts, 2);
-    const int es = dtype_size(src->dtype);
     void *pd = (char *)dst->data + dst->offset * es;
     const void *ps = (const char *)src->data + src->offset * es;
     const void *ptrs[3] = {pd, ps, nullptr};
@@ -957,6 +1092,7 @@ oxm_status oxm_convert(const oxm_view *src, const oxm_view *dst, void *stream) {
     DeviceGuard guard(src->device);
     if ((st = check_view_memory(src, "src", op)) != OXM_OK) return st;
     if ((st = check_view_memory(dst, "dst", op)) != OXM_OK) return st;
+    if ((st = refuse_overlap(span_of(dst), "destination", span_of(src), "source", op)) != OXM_OK) return st;
     const int64_t *sts[3] = {dst->strides, src->strides, nullptr};
     oxm::EwShape sh = collapse(src->ndim, src->shape, sts, 2);
     void *pd = (char *)dst->data + dst->offset * dtype_size(dst->dtype);
@@ -1008,6 +1144,11 @@ oxm_status oxm_sgd_step(const oxm_view *param, const oxm_view *grad, const oxm_v
     DeviceGuard guard(param->device);
     for (int i = 0; i < 3; ++i)
         if (vs[i] && (st = check_view_memory(vs[i], names[i], op)) != OXM_OK) return st;
+    // param and velocity are updated in place; no two of the three may share memory
+    for (int i = 0; i < 3; ++i)
+        for (int j = i + 1; j < 3; ++j)
+            if (vs[i] && vs[j] && (st = refuse_overlap(span_of(vs[i]), names[i], span_of(vs[j]), names[j], op)) != OXM_OK)
+                return st;
     void *pp = (char *)param->data + param->offset * dtype_size(param->dtype);
     const void *pg = (const char *)grad->data + grad->offset * dtype_size(grad->dtype);
     float *pv = velocity ? (float *)velocity->data + velocity->offset : nullptr;

@@ -42,6 +42,17 @@ def _np_dtype(dt: DType):
             DType.U8: np.uint8, DType.Bool: np.bool_, DType.BF16: np.uint16, DType.F16: np.float16}[dt]
 
 
+def _copy_stream(device: Device):
+    """The stream host copies of ``device`` run on: the registered backend's
+    current stream, so that a copy is ordered after the kernels queued there
+    (they may still read a recycled block, or produce the data being read);
+    None (synchronous, device-wide) when no backend stream is set."""
+    from .backend import _REGISTRY
+    be = _REGISTRY.get(device)
+    s = getattr(be, "stream", None) if be is not None else None
+    return C.c_void_p(s) if s else None
+
+
 # ---- storage -------------------------------------------------------------------
 
 
@@ -51,7 +62,11 @@ class _DevicePool:
     Freed blocks are kept per exact byte size and handed out again instead of
     calling hipFree (which synchronises the device).  Reuse is safe for work
     issued in stream order on one stream -- the backend's -- like PyTorch's
-    caching allocator; `release()` returns everything to HIP.
+    caching allocator: every op and every host copy (``from_numpy``,
+    ``to_numpy``) of a device runs on its backend's current stream, so a block
+    handed out again is written only after the work that last used it.  Work
+    issued on another stream must keep its tensors alive until that stream
+    is synchronised.  `release()` returns everything to HIP.
     """
 
     def __init__(self, device: int, cap_bytes: int = 64 << 30):
@@ -199,7 +214,7 @@ class Tensor:
             self._storage._host[:nbytes] = host.reshape(-1).view(np.uint8)
         else:
             check(_lib.lib().oxm_copy(C.c_void_p(self._storage.ptr), self.device.index,
-                                      C.c_void_p(host.ctypes.data), -1, nbytes, None))
+                                      C.c_void_p(host.ctypes.data), -1, nbytes, _copy_stream(self.device)))
 
     # -- accessors --
     @property
@@ -288,7 +303,7 @@ class Tensor:
             else:
                 check(_lib.lib().oxm_copy(C.c_void_p(buf.ctypes.data), -1,
                                           C.c_void_p(self._storage.ptr + lo * es), self.device.index,
-                                          nel * es, None))
+                                          nel * es, _copy_stream(self.device)))
             out = np.lib.stride_tricks.as_strided(buf[L.offset - lo:], shape=L.shape,
                                                   strides=tuple(s * es for s in L.strides)).copy()
         if self.dtype == DType.BF16:

@@ -49,6 +49,27 @@ class Operand:
         return widen(self.dtype, np.ascontiguousarray(v)).astype(np.float64)
 
 
+def _materialize(v: O.StridedView) -> np.ndarray:
+    """The view's elements (storage dtype) in logical order."""
+    es = v.buf.itemsize
+    return np.ascontiguousarray(np.lib.stride_tricks.as_strided(v.buf[v.offset:], shape=v.shape,
+                                                                strides=[s * es for s in v.strides]))
+
+
+def k_major(a: O.StridedView, b: O.StridedView) -> tuple[O.StridedView, O.StridedView]:
+    """The same logical operands with K contiguous on both sides (A row-major,
+    B the transpose of a row-major [.., N, K] copy).  The oracle sums each
+    output in ascending k whatever the layout, so its results are bit-for-bit
+    those of the original views; only its memory access pattern (and so its
+    speed on full-size checks) changes."""
+    am = _materialize(a)
+    bt = np.ascontiguousarray(np.swapaxes(_materialize(b), -1, -2))
+    av = O.StridedView.contiguous(am, a.dtype)
+    bv = O.StridedView.contiguous(bt, b.dtype)
+    perm = list(range(len(b.shape) - 2)) + [len(b.shape) - 1, len(b.shape) - 2]
+    return av, bv.permute(perm)
+
+
 def contiguous_operand(dtype, values, device=None):
     values = np.asarray(values, dtype=np.float32)
     shape = values.shape

@@ -267,3 +267,78 @@ def test_from_numpy_keeps_rank_zero():
     import oxmera_amd as ox
     t = ox.Tensor.from_numpy(np.array(2.5, np.float32), ox.Device.cpu())
     assert t.shape == () and t.to_numpy().shape == () and float(t.to_numpy()) == 2.5
+
+
+# ---- view byte ranges: overflow-checked (Tensor::from_storage's rule) ----------------
+
+def raw_view(shape, strides, offset=0, dtype=ox.DType.F32):
+    shp, st = _lib.i64_array(shape), _lib.i64_array(strides)
+    v = _lib.OxmView(C.c_void_p(0x1000), int(dtype), len(shape), C.cast(shp, C.POINTER(C.c_int64)),
+                     C.cast(st, C.POINTER(C.c_int64)), int(offset), 0)
+    v._keep = (shp, st)
+    return v
+
+
+def byte_range(v):
+    lo, hi = C.c_int64(0), C.c_int64(0)
+    st = _lib.lib().oxm_view_byte_range(C.byref(v), C.byref(lo), C.byref(hi))
+    return st, lo.value, hi.value
+
+
+def brute_range(shape, strides, offset, es):
+    """Every element's byte offset, enumerated (tiny views only)."""
+    offs = [offset]
+    for d, s in zip(shape, strides):
+        offs = [o + i * s for o in offs for i in range(d)]
+    return (min(offs) * es, (max(offs) + 1) * es) if offs and all(shape) else (0, 0)
+
+
+@pytest.mark.parametrize("shape,strides,offset,dtype", [
+    ([2, 3], [3, 1], 0, ox.DType.F32), ([2, 3], [1, 2], 5, ox.DType.BF16), ([3, 4], [-4, 1], 8, ox.DType.F32),
+    ([2, 2, 2], [0, -1, 7], 3, ox.DType.F64), ([5], [-2], 9, ox.DType.U8), ([0, 4], [4, 1], 0, ox.DType.F32),
+    ([], [], 6, ox.DType.I64), ([1, 1], [99, -99], 2, ox.DType.F16)])
+def test_view_byte_range_matches_enumeration(shape, strides, offset, dtype):
+    st, lo, hi = byte_range(raw_view(shape, strides, offset, dtype))
+    assert st == _lib.OK
+    assert (lo, hi) == brute_range(shape, strides, offset, dtype.size_in_bytes())
+
+
+@pytest.mark.parametrize("shape,strides,offset", [
+    ([2], [2 ** 61], 0),                  # (hi + 1) * 4 wraps to a negative byte count
+    ([3], [2 ** 62], 0),                  # the span itself overflows
+    ([2, 2], [-(2 ** 62), -(2 ** 62)], 0),  # the low end underflows
+    ([2], [1], 2 ** 63 - 1),              # offset + span overflows
+])
+def test_view_byte_range_refuses_overflow(shape, strides, offset):
+    st, _, _ = byte_range(raw_view(shape, strides, offset))
+    assert st == _lib.E_INDEX_OUT_OF_BOUNDS
+    assert "overflow" in _lib.last_error()
+
+
+def test_element_count_overflow_is_refused():
+    # 2^32 * 2^32 elements wraps int64 to 0: a view that would otherwise look empty
+    v = raw_view([2 ** 32, 2 ** 32], [1, 1])
+    st, _, _ = byte_range(v)
+    assert st == _lib.E_INDEX_OUT_OF_BOUNDS
+    a = raw_view([2 ** 32, 2 ** 32], [1, 1])
+    b = raw_view([2 ** 32, 2], [2, 1])
+    nd = C.c_int32(0)
+    out = (C.c_int64 * _lib.MAX_DIMS)()
+    assert _lib.lib().oxm_gemm_infer(C.byref(a), C.byref(b), C.byref(nd), out) == _lib.E_INDEX_OUT_OF_BOUNDS
+
+
+def test_epilogue_buffers_are_checked_on_the_host():
+    """bias / aux / colsum travel as raw pointers: Backend.matmul checks their
+    dtype, shape and layout before the call (typed errors, no device work)."""
+    be = ox.HipBackend(0)
+    a, b = host_tensor([4, 3]), host_tensor([3, 8])
+    with pytest.raises(ox.ShapeMismatch):
+        be.matmul(a, b, bias=host_tensor([4]))
+    with pytest.raises(ox.DTypeMismatch):
+        be.matmul(a, b, bias=host_tensor([8], ox.DType.I32))
+    with pytest.raises(ox.DTypeMismatch):
+        be.matmul(a, b, act=_lib.ACT_GELU, aux=host_tensor([4, 8], ox.DType.F16))
+    with pytest.raises(ox.NotImplementedOp):
+        be.matmul(a, b, act=_lib.ACT_GELU, aux=host_tensor([8, 4]).transpose_last())
+    with pytest.raises(ox.ShapeMismatch):
+        be.matmul(a, b, colsum=host_tensor([4]))

@@ -305,3 +305,29 @@ def test_colsum(oracle):
     got = oracle.colsum(x, oracle.F32)
     bound = 1.01 * 50 * 2.0 ** -24 * np.abs(x).sum(0)
     assert np.all(np.abs(got - x.astype(np.float64).sum(0)) <= bound)
+
+
+def test_k_major_copies_give_bit_identical_oracle_results(oracle):
+    """The full-size GPU checks hand the oracle K-contiguous copies of their
+    operands (tests/parity.k_major) for speed; each output is still summed in
+    ascending k, so the results must match the original views bit for bit."""
+    from tests.parity import k_major
+    O = oracle
+    rng = np.random.default_rng(12)
+    for dt, mk in ((O.F32, lambda x: x.astype(np.float32)), (O.BF16, O.bf16_round)):
+        abuf = mk(rng.normal(0, 1, 3 + 2 * 37 * 41))
+        bbuf = mk(rng.normal(0, 1, 41 * 29))
+        a = O.StridedView(abuf, dt, (37, 41), (2 * 41, 1), 3)           # every other row, offset
+        b = O.StridedView(bbuf, dt, (41, 29), (29, 1))                   # row-major B (N-contiguous)
+        bt = O.StridedView(bbuf, dt, (29, 41), (41, 1)).permute([1, 0])  # a transposed view
+        for bb in (b, bt):
+            want = O.matmul(a, bb)
+            got = O.matmul(*k_major(a, bb))
+            np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+        rows = np.array([0, 5, 36])
+        np.testing.assert_array_equal(O.matmul(*k_major(a, b), rows=rows), O.matmul(a, b, rows=rows))
+    # batched, broadcast B
+    abuf = rng.normal(0, 1, (3, 7, 11)).astype(np.float32)
+    bbuf = rng.normal(0, 1, (1, 11, 5)).astype(np.float32)
+    a, b = O.StridedView.contiguous(abuf), O.StridedView.contiguous(bbuf)
+    np.testing.assert_array_equal(O.matmul(*k_major(a, b)), O.matmul(a, b))
