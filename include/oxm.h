@@ -55,7 +55,11 @@ typedef enum {
     OXM_E_BACKEND_UNAVAILABLE = 8,    /* Error::BackendUnavailable     error.rs:85-90 */
     OXM_E_NOT_IMPLEMENTED = 9,        /* Error::NotImplemented         error.rs:92-101 */
     OXM_E_HIP = 10,
-    OXM_E_INVALID_ARGUMENT = 11
+    OXM_E_INVALID_ARGUMENT = 11,
+    /* The typed error BinaryOps::div promises for integer division by zero
+     * (crates/oxmera-ops/src/lib.rs:47-48).  oxmera_core::Error has no
+     * variant for it yet (the enum is #[non_exhaustive], error.rs:13). */
+    OXM_E_DIVISION_BY_ZERO = 12
 } oxm_status;
 
 /* oxmera_core::DType (dtype.rs:9-22) in declaration order, plus BF16 and F16,
@@ -173,10 +177,14 @@ oxm_status oxm_mse_loss_grad(const oxm_view *y, const oxm_view *t, const oxm_vie
                              const oxm_view *dy_colsum, void *stream);
 
 /* UnaryOps (crates/oxmera-ops/src/lib.rs:27-37): out = op(x) elementwise.
- * x: any strided view of F32/F64/BF16/F16 on a HIP device; out: a contiguous
- * view of x's shape and dtype ("a fresh contiguous tensor", :16-17).  exp
- * and ln follow the device's IEEE-754 float functions (ln of a negative is
- * NaN, of zero -inf). */
+ * x: any strided view on a HIP device; out: a contiguous view of x's shape
+ * and dtype ("a fresh contiguous tensor", :16-17).  Float dtypes (F32, F64,
+ * BF16, F16): every op; exp and ln follow the device's IEEE-754 float
+ * functions (ln of a negative is NaN, of zero -inf).  I32 / I64 / U8: neg
+ * and abs, wrapping (neg(i32::MIN) = abs(i32::MIN) = i32::MIN, neg of a U8
+ * is 256 - x mod 256); Bool: abs (the identity).  exp and ln are "float
+ * dtypes only" (:31-34): OXM_E_UNSUPPORTED_DTYPE, as is any other
+ * unsupported pairing. */
 typedef enum {
     OXM_UN_NEG = 0,
     OXM_UN_EXP = 1,
@@ -190,8 +198,13 @@ oxm_status oxm_unary(int32_t op, const oxm_view *x, const oxm_view *out, void *s
 
 /* BinaryOps (crates/oxmera-ops/src/lib.rs:39-50): out = a op b with NumPy
  * broadcasting (crates/oxmera-core/src/shape.rs:45-58; BroadcastIncompatible
- * otherwise).  a, b: same dtype (F32/F64/BF16/F16) and device, any strides;
- * out: contiguous, the broadcast shape.  Float division follows IEEE-754. */
+ * otherwise).  a, b: same dtype and device, any strides; out: contiguous,
+ * the broadcast shape.  Float division follows IEEE-754.  I32 / I64 / U8:
+ * add, sub, mul wrap; div truncates toward zero (i32::MIN / -1 wraps to
+ * i32::MIN) and a zero divisor anywhere is OXM_E_DIVISION_BY_ZERO (integer
+ * div then runs synchronously on `stream`, to know it before returning;
+ * the output holds 0 where the divisor was 0).  Bool: add is OR, mul is
+ * AND; sub and div are OXM_E_UNSUPPORTED_DTYPE.  eq: every dtype. */
 typedef enum {
     OXM_BIN_ADD = 0,
     OXM_BIN_SUB = 1,
@@ -208,8 +221,10 @@ oxm_status oxm_binary(int32_t op, const oxm_view *a, const oxm_view *b, const ox
 
 /* ReduceOps (crates/oxmera-ops/src/lib.rs:61-69): sum or max over `axes`,
  * removing them from the shape; naxes == 0 means every axis (a rank-0
- * result).  Accumulation in f32 (f64 for F64), one rounding to the output
- * dtype, a fixed combination order (results do not depend on scheduling).
+ * result).  Float dtypes: accumulation in f32 (f64 for F64), one rounding to
+ * the output dtype, a fixed combination order (results do not depend on
+ * scheduling).  I32 / I64 / U8: sum wraps in the dtype (the exact sum modulo
+ * 2^bits, whatever the order), max is exact; Bool: sum and max are OR.
  * max propagates NaN and refuses an empty reduced extent (ShapeMismatch:
  * "there is no identity to invent").  oxm_reduce_infer gives the output
  * shape; out must be contiguous with it and x's dtype. */

@@ -120,3 +120,91 @@ def reduced_shape(shape, axes) -> tuple:
     if not len(axes):
         return ()
     return tuple(e for d, e in enumerate(shape) if d not in set(axes))
+
+
+# ---- integer and boolean dtypes ------------------------------------------------
+# The reference's DType carries I32, I64, U8 and Bool (crates/oxmera-core/src/
+# dtype.rs:9-22) but specifies no integer semantics beyond "integer division
+# by zero is a typed error" (crates/oxmera-ops/src/lib.rs:47-48).  The build
+# defines them as Rust's wrapping arithmetic on fixed-width integers (NumPy's
+# fixed-width integer arithmetic is the same), `/` truncating toward zero,
+# and Bool as a 0/1 byte with add = OR, mul = AND.  Restated with explicit
+# integer operations here (no float round trips), so results are exact.
+
+I32, I64, U8, BOOL = 2, 3, 4, 5
+INT_NP = {I32: np.int32, I64: np.int64, U8: np.uint8, BOOL: np.uint8}
+BIN_EQ = 4
+
+
+class DivisionByZero(Exception):
+    """Integer division by zero (the typed error of BinaryOps::div)."""
+
+
+def _wrap(x: np.ndarray, dtype: int) -> np.ndarray:
+    """Reduce an int64-or-object array modulo 2^bits into the dtype."""
+    t = INT_NP[dtype]
+    bits = np.iinfo(t).bits
+    v = np.asarray(np.asarray(x, dtype=object) % (1 << bits), dtype=object)
+    if np.iinfo(t).min < 0:
+        v = np.asarray(np.where(v >= (1 << (bits - 1)), v - (1 << bits), v), dtype=object)
+    return v.astype(t)
+
+
+def int_unary(x: np.ndarray, op: int, dtype: int) -> np.ndarray:
+    """neg / abs, wrapping; Bool: abs only (the identity)."""
+    xo = np.asarray(x).astype(object)
+    if dtype == BOOL:
+        if op != UN_ABS:
+            raise ValueError("Bool carries abs only")
+        return np.asarray(x).copy()
+    if op == UN_NEG:
+        return _wrap(-xo, dtype)
+    if op == UN_ABS:
+        return _wrap(np.abs(xo), dtype)
+    raise ValueError("integer dtypes carry neg and abs only")
+
+
+def _trunc_div(a: int, b: int) -> int:
+    q = abs(a) // abs(b)
+    return q if (a >= 0) == (b >= 0) else -q
+
+
+def int_binary(a: np.ndarray, b: np.ndarray, op: int, dtype: int) -> np.ndarray:
+    """add / sub / mul / div / eq with broadcasting; wrapping; div truncates
+    toward zero and raises DivisionByZero for any zero divisor."""
+    a, b = np.broadcast_arrays(np.asarray(a), np.asarray(b))
+    if op == BIN_EQ:
+        return (a == b).astype(INT_NP[dtype])
+    if dtype == BOOL:
+        if op == BIN_ADD:
+            return ((a != 0) | (b != 0)).astype(np.uint8)
+        if op == BIN_MUL:
+            return ((a != 0) & (b != 0)).astype(np.uint8)
+        raise ValueError("Bool carries add, mul and eq only")
+    ao, bo = a.astype(object), b.astype(object)
+    if op == BIN_ADD:
+        return _wrap(ao + bo, dtype)
+    if op == BIN_SUB:
+        return _wrap(ao - bo, dtype)
+    if op == BIN_MUL:
+        return _wrap(ao * bo, dtype)
+    if op == BIN_DIV:
+        if np.any(b == 0):
+            raise DivisionByZero("integer division by zero")
+        q = np.frompyfunc(_trunc_div, 2, 1)(ao, bo)
+        return _wrap(q, dtype)
+    raise ValueError(op)
+
+
+def int_reduce(x: np.ndarray, axes, op: int, dtype: int) -> np.ndarray:
+    """sum (exact, then wrapped into the dtype) or max over `axes` (all when
+    empty); Bool: both are OR.  max over an empty extent has no identity."""
+    x = np.asarray(x)
+    ax = tuple(range(x.ndim)) if len(axes) == 0 else tuple(axes)
+    if dtype == BOOL:
+        return np.any(x != 0, axis=ax).astype(np.uint8)
+    if op == 0:  # sum
+        return _wrap(np.sum(x.astype(object), axis=ax), dtype)
+    if any(x.shape[a] == 0 for a in ax):
+        raise ValueError("max over an empty extent")
+    return np.max(x, axis=ax)

@@ -10,8 +10,8 @@ Layers:
   ``autograd``/``nn``/``optim``  the tape, Linear layers and SGD.
 """
 from . import _lib
-from .core import (BackendUnavailable, BroadcastIncompatible, Device, DeviceMismatch, DType, DTypeMismatch,
-                   HipError, IndexOutOfBounds, InvalidArgument, Layout, NotImplementedOp, OxmError, RankMismatch,
+from .core import (BackendUnavailable, BroadcastIncompatible, Device, DeviceMismatch, DivisionByZero, DType,
+                   DTypeMismatch, HipError, IndexOutOfBounds, InvalidArgument, Layout, NotImplementedOp, OxmError, RankMismatch,
                    ShapeMismatch, UnsupportedDType, broadcast_shapes, contiguous_strides, numel)
 from .tensor import Storage, Tensor, bf16_bits_to_f32, f32_to_bf16_bits
 from .backend import HipBackend, backend_for, device_count, init, register_backend
@@ -19,7 +19,8 @@ from .backend import HipBackend, backend_for, device_count, init, register_backe
 ACT_NONE, ACT_GELU, ACT_DGELU = _lib.ACT_NONE, _lib.ACT_GELU, _lib.ACT_DGELU
 
 __all__ = [
-    "BackendUnavailable", "BroadcastIncompatible", "Device", "DeviceMismatch", "DType", "DTypeMismatch",
+    "BackendUnavailable", "BroadcastIncompatible", "Device", "DeviceMismatch", "DivisionByZero", "DType",
+    "DTypeMismatch",
     "HipError", "IndexOutOfBounds", "InvalidArgument", "Layout", "NotImplementedOp", "OxmError", "RankMismatch",
     "ShapeMismatch", "UnsupportedDType", "broadcast_shapes", "contiguous_strides", "numel", "Storage", "Tensor",
     "bf16_bits_to_f32", "f32_to_bf16_bits", "HipBackend", "backend_for", "device_count", "init",

@@ -27,6 +27,7 @@ E_BACKEND_UNAVAILABLE = 8
 E_NOT_IMPLEMENTED = 9
 E_HIP = 10
 E_INVALID_ARGUMENT = 11
+E_DIVISION_BY_ZERO = 12
 
 # oxm_act
 ACT_NONE = 0

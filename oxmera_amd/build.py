@@ -24,7 +24,7 @@ LIB = PKG / "liboxm.so"
 ARCH = os.environ.get("OXM_GFX", "gfx950")
 
 SOURCES = ["oxm_capi.cpp", "gemm.hip", "gemm_f32.hip", "gemm_bf16.hip", "gemm_f16.hip", "gemm_strip.hip",
-           "glue.hip", "elementwise.hip"]
+           "glue.hip", "elementwise.hip", "elementwise_int.hip"]
 
 # -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 on this pool.
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
@@ -71,15 +71,25 @@ def build_cli(verbose: bool = True) -> Path:
     return CLI
 
 
+def _deps(path: Path, seen: set) -> set:
+    """The file and every local header it includes, transitively."""
+    import re
+    if path in seen or not path.exists():
+        return seen
+    seen.add(path)
+    for inc in re.findall(r'^\s*#\s*include\s+"([^"]+)"', path.read_text(), re.M):
+        _deps((path.parent / inc).resolve(), seen)
+    return seen
+
+
 def _stale(src: str) -> bool:
-    """Whether a unit's object is older than its source or any header under
-    csrc/ or include/ (a unit includes only those)."""
+    """Whether a unit's object is older than its source or a header it
+    includes."""
     obj = BUILD / (src.replace(".", "_") + ".o")
     if not obj.exists():
         return True
     t = obj.stat().st_mtime
-    deps = [CSRC / src, *CSRC.glob("*.hpp"), *(PKG.parent / "include").glob("*.h")]
-    return any(d.stat().st_mtime > t for d in deps)
+    return any(d.stat().st_mtime > t for d in _deps((CSRC / src).resolve(), set()))
 
 
 def build(verbose: bool = True, changed_only: bool = False) -> Path:

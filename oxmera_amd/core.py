@@ -131,9 +131,15 @@ class InvalidArgument(OxmError):
     code = _lib.E_INVALID_ARGUMENT
 
 
+class DivisionByZero(OxmError):
+    """Integer division by zero: the typed error BinaryOps::div promises
+    (crates/oxmera-ops/src/lib.rs:47-48)."""
+    code = _lib.E_DIVISION_BY_ZERO
+
+
 _BY_CODE = {cls.code: cls for cls in (ShapeMismatch, BroadcastIncompatible, DTypeMismatch, UnsupportedDType,
                                       DeviceMismatch, IndexOutOfBounds, RankMismatch, BackendUnavailable,
-                                      NotImplementedOp, HipError, InvalidArgument)}
+                                      NotImplementedOp, HipError, InvalidArgument, DivisionByZero)}
 
 
 def check(status: int) -> None:

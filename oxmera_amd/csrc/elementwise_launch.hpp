@@ -6,6 +6,7 @@
 namespace oxm {
 
 constexpr int kDtF64 = 1;  // oxm_dtype F64 (F32 = 0, BF16 = 6, F16 = 7 are in gemm_kernels.hpp)
+constexpr int kDtI32 = 2, kDtI64 = 3, kDtU8 = 4, kDtBool = 5;  // oxm_dtype integer / boolean codes
 
 enum UnaryOp : int { kUnNeg = 0, kUnExp = 1, kUnLn = 2, kUnAbs = 3, kUnSign = 4 };
 enum BinaryOp : int { kBinAdd = 0, kBinSub = 1, kBinMul = 2, kBinDiv = 3, kBinEq = 4, kBinDGelu = 5 };
@@ -48,6 +49,14 @@ hipError_t launch_elementwise(int dtype, int nops, int op, const EwShape &s, voi
 hipError_t launch_copy(int elem_bytes, const EwShape &s, void *dst, const void *src, bool contig16, hipStream_t st);
 
 hipError_t launch_reduce(int dtype, int op, const RedGeom &g, const void *x, void *out, hipStream_t st);
+
+// The same for I32 / I64 / U8 / Bool (elementwise_int.hip): unary neg / abs,
+// binary add / sub / mul / div / eq, reduce sum / max; the host has refused
+// the combinations a dtype does not carry.  Integer div stores 1 to
+// *zero_div (a device int the caller cleared) when a divisor is zero.
+hipError_t launch_elementwise_int(int dtype, int nops, int op, const EwShape &s, void *out, const void *x,
+                                  const void *y, int *zero_div, hipStream_t st);
+hipError_t launch_reduce_int(int dtype, int op, const RedGeom &g, const void *x, void *out, hipStream_t st);
 
 // dst = src converted from dtype dti to dtype dto (float dtypes); operand 0
 // of s is dst, operand 1 src.

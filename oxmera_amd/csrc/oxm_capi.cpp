@@ -338,6 +338,17 @@ int env_int(const char *name, int dflt) {
 }
 
 bool is_float_dtype(int dt) { return dt == OXM_F32 || dt == OXM_F64 || dt == OXM_BF16 || dt == OXM_F16; }
+bool is_int_dtype(int dt) { return dt == OXM_I32 || dt == OXM_I64 || dt == OXM_U8 || dt == OXM_BOOL; }
+
+// Which ops the integer and boolean dtypes carry (elementwise_int.hip): neg
+// and abs, add / sub / mul / div / eq, sum and max; Bool has no neg, sub or
+// div (NumPy refuses them too).  exp and ln are "float dtypes only"
+// (crates/oxmera-ops/src/lib.rs:31-34); sign and dgelu serve the float tape.
+bool int_unary_ok(int dt, int op) { return op == OXM_UN_ABS || (op == OXM_UN_NEG && dt != OXM_BOOL); }
+bool int_binary_ok(int dt, int op) {
+    if (op == OXM_BIN_ADD || op == OXM_BIN_MUL || op == OXM_BIN_EQ) return true;
+    return (op == OXM_BIN_SUB || op == OXM_BIN_DIV) && dt != OXM_BOOL;
+}
 
 // Row-major iteration space over `shape` for up to three operands (0 = the
 // output), dims of extent 1 dropped and neighbours merged where every
@@ -424,6 +435,29 @@ oxm_status check_out(const oxm_view *out, int dtype, int nd, const int64_t *shap
         return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s vs %s in %s", device_str(device).c_str(),
                     device_str(out->device).c_str(), op);
     return OXM_OK;
+}
+
+// Integer division with its typed refusal of a zero divisor (BinaryOps::div,
+// crates/oxmera-ops/src/lib.rs:47-48): the kernel raises a device flag,
+// which is read back after the stream has run it, so this call is
+// synchronous on `s` whatever the stream (the error has to be known when the
+// call returns).  The output holds 0 where a divisor was 0.
+oxm_status int_div(const oxm::EwShape &sh, int dtype, void *po, const void *pa, const void *pb, hipStream_t s) {
+    const char *op = "div";
+    int *flag = nullptr;
+    hipError_t e = hipMallocAsync((void **)&flag, sizeof(int), s);
+    if (e != hipSuccess) return hip_fail(e, op);
+    int host_flag = 0;
+    e = oxm::launch_fill_zero((float *)flag, 1, s);  // a fill kernel, not a memset node (graph-safe)
+    if (e == hipSuccess) e = oxm::launch_elementwise_int(dtype, 2, OXM_BIN_DIV, sh, po, pa, pb, flag, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(&host_flag, flag, sizeof(int), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    hipError_t f = hipFreeAsync(flag, s);
+    if (e == hipSuccess) e = f;
+    if (e != hipSuccess) return hip_fail(e, op);
+    if (host_flag)
+        return fail(OXM_E_DIVISION_BY_ZERO, "integer division by zero in div (dtype %s)", dtype_name(dtype));
+    return ok();
 }
 
 }  // namespace
@@ -858,7 +892,7 @@ oxm_status oxm_unary(int32_t op, const oxm_view *x, const oxm_view *out, void *s
     oxm_status st;
     if ((st = check_view(x, "input", name)) != OXM_OK) return st;
     if ((st = check_view(out, "out", name)) != OXM_OK) return st;
-    if (!is_float_dtype(x->dtype))
+    if (!is_float_dtype(x->dtype) && !(is_int_dtype(x->dtype) && int_unary_ok(x->dtype, op)))
         return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by %s", dtype_name(x->dtype), name);
     if (x->device < 0) return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s is not a HIP device in %s",
                                    device_str(x->device).c_str(), name);
@@ -883,7 +917,9 @@ oxm_status oxm_unary(int32_t op, const oxm_view *x, const oxm_view *out, void *s
     const void *px = (const char *)x->data + x->offset * es;
     const void *ptrs[3] = {po, px, nullptr};
     hipStream_t s = (hipStream_t)stream;
-    hipError_t e = oxm::launch_elementwise(x->dtype, 1, op, sh, po, px, nullptr, ew_vec(sh, 2, ptrs, es), s);
+    hipError_t e = is_int_dtype(x->dtype)
+                       ? oxm::launch_elementwise_int(x->dtype, 1, op, sh, po, px, nullptr, nullptr, s)
+                       : oxm::launch_elementwise(x->dtype, 1, op, sh, po, px, nullptr, ew_vec(sh, 2, ptrs, es), s);
     if (e != hipSuccess) return hip_fail(e, name);
     return finish(s, name);
 }
@@ -898,7 +934,7 @@ oxm_status oxm_binary(int32_t op, const oxm_view *a, const oxm_view *b, const ox
     if (a->dtype != b->dtype)
         return fail(OXM_E_DTYPE_MISMATCH, "dtype mismatch: expected %s, got %s in %s", dtype_name(a->dtype),
                     dtype_name(b->dtype), name);
-    if (!is_float_dtype(a->dtype))
+    if (!is_float_dtype(a->dtype) && !(is_int_dtype(a->dtype) && int_binary_ok(a->dtype, op)))
         return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by %s", dtype_name(a->dtype), name);
     if (a->device != b->device)
         return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s vs %s in %s", device_str(a->device).c_str(),
@@ -939,6 +975,14 @@ oxm_status oxm_binary(int32_t op, const oxm_view *a, const oxm_view *b, const ox
     const void *pa = (const char *)a->data + a->offset * es, *pb = (const char *)b->data + b->offset * es;
     const void *ptrs[3] = {po, pa, pb};
     hipStream_t s = (hipStream_t)stream;
+    if (is_int_dtype(a->dtype)) {
+        if (op != OXM_BIN_DIV) {
+            hipError_t e = oxm::launch_elementwise_int(a->dtype, 2, op, sh, po, pa, pb, nullptr, s);
+            if (e != hipSuccess) return hip_fail(e, name);
+            return finish(s, name);
+        }
+        return int_div(sh, a->dtype, po, pa, pb, s);
+    }
     hipError_t e = oxm::launch_elementwise(a->dtype, 2, op, sh, po, pa, pb, ew_vec(sh, 3, ptrs, es), s);
     if (e != hipSuccess) return hip_fail(e, name);
     return finish(s, name);
@@ -976,7 +1020,7 @@ oxm_status oxm_reduce(int32_t op, const oxm_view *x, const int32_t *axes, int32_
     int64_t oshape[OXM_MAX_DIMS];
     if ((st = oxm_reduce_infer(x, axes, naxes, &nd, oshape)) != OXM_OK) return st;
     if ((st = check_view(out, "out", name)) != OXM_OK) return st;
-    if (!is_float_dtype(x->dtype))
+    if (!is_float_dtype(x->dtype) && !is_int_dtype(x->dtype))
         return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by %s", dtype_name(x->dtype), name);
     if (x->device < 0) return fail(OXM_E_DEVICE_MISMATCH, "device mismatch: %s is not a HIP device in %s",
                                    device_str(x->device).c_str(), name);
@@ -1028,8 +1072,11 @@ oxm_status oxm_reduce(int32_t op, const oxm_view *x, const int32_t *axes, int32_
     }
     const int es = dtype_size(x->dtype);
     hipStream_t s = (hipStream_t)stream;
-    hipError_t e = oxm::launch_reduce(x->dtype, op, g, (const char *)x->data + x->offset * es,
-                                      (char *)out->data + out->offset * es, s);
+    hipError_t e = is_int_dtype(x->dtype)
+                       ? oxm::launch_reduce_int(x->dtype, op, g, (const char *)x->data + x->offset * es,
+                                                (char *)out->data + out->offset * es, s)
+                       : oxm::launch_reduce(x->dtype, op, g, (const char *)x->data + x->offset * es,
+                                            (char *)out->data + out->offset * es, s);
     if (e != hipSuccess) return hip_fail(e, name);
     return finish(s, name);
 }

@@ -108,15 +108,26 @@ def test_reduce_convert_copy_and_sgd_refuse_overlap(hip):
     assert _lib.lib().oxm_copy(C.c_void_p(base + 16), 0, C.c_void_p(base), 0, 1024, None) == _lib.E_INVALID_ARGUMENT
 
 
+def _hip_runtime():
+    """The HIP runtime library liboxm.so itself uses (already mapped into the
+    process), for creating a plain non-blocking stream without torch."""
+    for line in open("/proc/self/maps"):
+        path = line.split()[-1]
+        if "libamdhip64.so" in path and "/torch/" not in path:
+            return C.CDLL(path)
+    raise RuntimeError("libamdhip64 is not mapped: liboxm.so was not loaded")
+
+
 def test_host_copies_follow_the_backend_stream(hip):
     """With a non-default backend stream, from_numpy / to_numpy are ordered
     after the kernels queued on it (a recycled block is not overwritten under
     a pending kernel; a read-back sees the finished result)."""
-    import torch
     print("host copies on the backend stream", flush=True)
     rng = np.random.default_rng(5)
-    s = torch.cuda.Stream()
-    hip.set_stream(s.cuda_stream)
+    rt = _hip_runtime()
+    stream = C.c_void_p()
+    assert rt.hipStreamCreateWithFlags(C.byref(stream), 1) == 0  # hipStreamNonBlocking, default priority
+    hip.set_stream(stream.value)
     try:
         x = rng.normal(0, 1, (2048, 2048)).astype(np.float32)
         a = dev(x)
@@ -130,3 +141,5 @@ def test_host_copies_follow_the_backend_stream(hip):
         np.testing.assert_array_equal(b.to_numpy(), np.ones((2048, 2048), np.float32))
     finally:
         hip.set_stream(None)
+        assert rt.hipStreamSynchronize(stream) == 0
+        assert rt.hipStreamDestroy(stream) == 0

@@ -129,3 +129,83 @@ def test_max_closed_forms_and_nan():
         R.reduce_max(np.zeros((3, 0), np.float32), [1], R.F32)
     s, _ = R.reduce_sum_f64(np.zeros((3, 0), np.float32), [1], R.F32)
     assert s.tolist() == [0, 0, 0]
+
+
+# ---- integer / boolean semantics (oracle/ops_ref.py int_*) ----------------------------
+# Pinned by hand-worked cases and by the arithmetic identities that fix
+# wrapping and truncating division, not by restating the oracle's formulas.
+
+def test_int_hand_cases():
+    i32 = lambda *v: np.array(v, np.int32)
+    # truncation toward zero in every sign combination; MIN / -1 wraps
+    np.testing.assert_array_equal(R.int_binary(i32(7, -7, 7, -7, -2 ** 31), i32(2, 2, -2, -2, -1), R.BIN_DIV, R.I32),
+                                  i32(3, -3, -3, 3, -2 ** 31))
+    np.testing.assert_array_equal(R.int_binary(i32(2 ** 31 - 1), i32(1), R.BIN_ADD, R.I32), i32(-2 ** 31))
+    np.testing.assert_array_equal(R.int_binary(i32(-2 ** 31), i32(1), R.BIN_SUB, R.I32), i32(2 ** 31 - 1))
+    np.testing.assert_array_equal(R.int_binary(i32(65536), i32(65536), R.BIN_MUL, R.I32), i32(0))
+    np.testing.assert_array_equal(R.int_unary(i32(-2 ** 31, -5, 0, 5), R.UN_ABS, R.I32), i32(-2 ** 31, 5, 0, 5))
+    np.testing.assert_array_equal(R.int_unary(i32(-2 ** 31, -5, 0), R.UN_NEG, R.I32), i32(-2 ** 31, 5, 0))
+    u8 = lambda *v: np.array(v, np.uint8)
+    np.testing.assert_array_equal(R.int_binary(u8(250, 3), u8(10, 5), R.BIN_ADD, R.U8), u8(4, 8))
+    np.testing.assert_array_equal(R.int_binary(u8(3), u8(5), R.BIN_SUB, R.U8), u8(254))
+    np.testing.assert_array_equal(R.int_unary(u8(0, 1, 255), R.UN_NEG, R.U8), u8(0, 255, 1))
+    np.testing.assert_array_equal(R.int_binary(u8(255, 7), u8(16, 2), R.BIN_DIV, R.U8), u8(15, 3))
+    i64 = lambda *v: np.array(v, np.int64)
+    np.testing.assert_array_equal(R.int_binary(i64(2 ** 62), i64(4), R.BIN_MUL, R.I64), i64(0))
+    np.testing.assert_array_equal(R.int_binary(i64(-2 ** 63), i64(-1), R.BIN_DIV, R.I64), i64(-2 ** 63))
+    b = lambda *v: np.array(v, np.uint8)
+    np.testing.assert_array_equal(R.int_binary(b(0, 0, 1, 1), b(0, 1, 0, 1), R.BIN_ADD, R.BOOL), b(0, 1, 1, 1))
+    np.testing.assert_array_equal(R.int_binary(b(0, 0, 1, 1), b(0, 1, 0, 1), R.BIN_MUL, R.BOOL), b(0, 0, 0, 1))
+    np.testing.assert_array_equal(R.int_binary(b(0, 0, 1, 1), b(0, 1, 0, 1), R.BIN_EQ, R.BOOL), b(1, 0, 0, 1))
+    with pytest.raises(R.DivisionByZero):
+        R.int_binary(i32(1, 2), i32(1, 0), R.BIN_DIV, R.I32)
+
+
+@pytest.mark.parametrize("dt,np_t", [(R.I32, np.int32), (R.I64, np.int64), (R.U8, np.uint8)])
+def test_int_identities(dt, np_t):
+    rng = np.random.default_rng(dt)
+    info = np.iinfo(np_t)
+    a = rng.integers(info.min, info.max, 500, dtype=np_t, endpoint=True)
+    b = rng.integers(info.min, info.max, 500, dtype=np_t, endpoint=True)
+    b[b == 0] = 1
+    mod = 1 << info.bits
+    # wrapping = the exact result reduced modulo 2^bits
+    for op, f in ((R.BIN_ADD, lambda x, y: x + y), (R.BIN_SUB, lambda x, y: x - y), (R.BIN_MUL, lambda x, y: x * y)):
+        got = R.int_binary(a, b, op, dt)
+        for x, y, g in zip(a.tolist(), b.tolist(), got.tolist()):
+            assert (f(x, y) - g) % mod == 0
+            assert info.min <= g <= info.max
+    # a + neg(a) == 0; abs(a) == a or neg(a)
+    z = R.int_binary(a, R.int_unary(a, R.UN_NEG, dt), R.BIN_ADD, dt)
+    assert not z.any()
+    ab = R.int_unary(a, R.UN_ABS, dt)
+    assert np.all((ab == a) | (ab == R.int_unary(a, R.UN_NEG, dt)))
+    # truncating division: a = q*b + r, |r| < |b|, r has a's sign (or is 0)
+    q = R.int_binary(a, b, R.BIN_DIV, dt)
+    for x, y, qq in zip(a.tolist(), b.tolist(), q.tolist()):
+        if np_t != np.uint8 and x == info.min and y == -1:
+            assert qq == info.min
+            continue
+        r = x - qq * y
+        assert abs(r) < abs(y) and (r == 0 or (r > 0) == (x > 0))
+
+
+def test_int_reductions_closed_forms():
+    # sum of 0..n-1 = n(n-1)/2, wrapped into I32; order does not matter
+    n = 100_000
+    x = np.arange(n, dtype=np.int32).reshape(250, 400)
+    want = (n * (n - 1) // 2) % (1 << 32)
+    want = want - (1 << 32) if want >= (1 << 31) else want
+    assert int(R.int_reduce(x, [], 0, R.I32)) == want
+    perm = np.random.default_rng(0).permutation(n).astype(np.int32).reshape(250, 400)
+    assert int(R.int_reduce(perm, [], 0, R.I32)) == want
+    np.testing.assert_array_equal(R.int_reduce(x, [1], 0, R.I64 if False else R.I32),
+                                  (400 * np.arange(250, dtype=np.int64) * 400 + 400 * 399 // 2).astype(np.int32))
+    # max is the last of a sorted copy; Bool sum / max are any()
+    y = np.random.default_rng(1).integers(-50, 50, (7, 9)).astype(np.int64)
+    np.testing.assert_array_equal(R.int_reduce(y, [0], 1, R.I64), np.sort(y, axis=0)[-1])
+    bb = np.array([[0, 0, 1], [0, 0, 0]], np.uint8)
+    np.testing.assert_array_equal(R.int_reduce(bb, [1], 0, R.BOOL), [1, 0])
+    np.testing.assert_array_equal(R.int_reduce(bb, [0], 1, R.BOOL), [0, 0, 1])
+    # U8 sum wraps modulo 256
+    assert int(R.int_reduce(np.full(300, 255, np.uint8), [], 0, R.U8)) == (300 * 255) % 256
