@@ -125,8 +125,13 @@ def test_binary_refusals(hip):
         ox.Tensor.empty((2, 3), ox.DType.F32, d).add(ox.Tensor.empty((4,), ox.DType.F32, d))
     with pytest.raises(ox.DTypeMismatch):
         ox.Tensor.empty((2, 3), ox.DType.F32, d).mul(ox.Tensor.empty((2, 3), ox.DType.BF16, d))
+    # integer dtypes carry neg / abs and add / sub / mul / div / eq
+    # (tests/test_gpu_int_ops.py); exp and ln are "float dtypes only"
+    # (crates/oxmera-ops/src/lib.rs:31-34), Bool has no neg
     with pytest.raises(ox.UnsupportedDType):
-        ox.Tensor.empty((2, 3), ox.DType.I32, d).neg()
+        ox.Tensor.empty((2, 3), ox.DType.I32, d).exp()
+    with pytest.raises(ox.UnsupportedDType):
+        ox.Tensor.empty((2, 3), ox.DType.Bool, d).neg()
 
 
 def test_division_ieee(hip):
