@@ -234,6 +234,21 @@ oxm_status oxm_reduce_infer(const oxm_view *x, const int32_t *axes, int32_t naxe
 oxm_status oxm_reduce(int32_t op, const oxm_view *x, const int32_t *axes, int32_t naxes, const oxm_view *out,
                       void *stream);
 
+/* oxm_reduce with no allocation: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): the partial results
+ * of a split reduction go to a static per-GPU scratch area of
+ * OXM_REDUCE_SCRATCH_BYTES that the library holds until the process ends,
+ * instead of a stream allocation, and the call allocates nothing (integer
+ * reductions never need it).  Same arguments, checks and results as
+ * oxm_reduce; a reduction whose partials would not fit is
+ * OXM_E_NOT_IMPLEMENTED.  Every call on one GPU shares that GPU's scratch:
+ * calls that overlap in time on one GPU (other threads, other streams) race
+ * and must be serialised by the caller. */
+#define OXM_REDUCE_SCRATCH_BYTES (8u << 20)
+oxm_status oxm_reduce_noalloc(int32_t op, const oxm_view *x, const int32_t *axes, int32_t naxes,
+                              const oxm_view *out, void *stream);
+
 /* Tensor::contiguous's copy (crates/oxmera-tensor/src/tensor.rs:86-90):
  * dst = src element by element, bits unchanged.  Same shape and dtype, same
  * HIP device; src any strides, dst any strides that do not repeat elements

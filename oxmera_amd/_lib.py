@@ -83,6 +83,8 @@ _PROTOS = {
                                    C.POINTER(C.c_int64)]),
     "oxm_reduce": (C.c_int, [C.c_int32, C.POINTER(OxmView), C.POINTER(C.c_int32), C.c_int32, C.POINTER(OxmView),
                              C.c_void_p]),
+    "oxm_reduce_noalloc": (C.c_int, [C.c_int32, C.POINTER(OxmView), C.POINTER(C.c_int32), C.c_int32,
+                                     C.POINTER(OxmView), C.c_void_p]),
     "oxm_copy_view": (C.c_int, [C.POINTER(OxmView), C.POINTER(OxmView), C.c_void_p]),
     "oxm_convert": (C.c_int, [C.POINTER(OxmView), C.POINTER(OxmView), C.c_void_p]),
     "oxm_sgd_step": (C.c_int, [C.POINTER(OxmView), C.POINTER(OxmView), C.POINTER(OxmView), C.c_float, C.c_float,

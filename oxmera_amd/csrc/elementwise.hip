@@ -18,6 +18,8 @@
 // thread and may split the reduced range over blocks, writing partials to a
 // workspace that a second pass combines in a fixed order -- no atomics, so
 // results do not depend on scheduling.  Other layouts: a thread per output.
+#include <mutex>
+
 #include "elementwise_launch.hpp"
 #include "gemm_kernels.hpp"
 
@@ -823,45 +825,74 @@ hipError_t ew_dispatch(int nops, int op, const EwShape &s, void *out, const void
     }
 }
 
-template <int DT, int OP>
-hipError_t red_launch(const RedGeom &g, const void *x, void *out, hipStream_t st) {
-    using A = typename El<DT>::Acc;
-    if (g.n_out == 0) return hipSuccess;
-    const bool rows = g.nr == 1 && g.rst[0] == 1 && g.n_red >= 256;
-    const bool cols = !rows && g.kst[g.nk - 1] == 1 && g.n_out >= 64 && g.n_red >= 2 * kRedU;
+// How a reduction is scheduled (red_launch): rows, columns (with 16-byte
+// loads when cols_vec), or a thread per output; splits > 1 combines partial
+// results from a workspace of sizeof(Acc) * n_out * splits bytes.
+struct RedPlan {
+    bool rows, cols, cols_vec;
+    int64_t splits;
+};
+
+template <int DT>
+RedPlan plan_reduce(const RedGeom &g, const void *x) {
+    RedPlan pl{};
+    pl.rows = g.nr == 1 && g.rst[0] == 1 && g.n_red >= 256;
+    pl.cols = !pl.rows && g.kst[g.nk - 1] == 1 && g.n_out >= 64 && g.n_red >= 2 * kRedU;
     // column schedule with 16-byte loads: every V-group of consecutive
     // outputs starts 16-byte aligned at every reduced element (x aligned, the
     // innermost kept dim a multiple of V long, every other stride a multiple
     // of V)
-    bool cols_vec = false;
+    pl.cols_vec = false;
     if constexpr (DT != kDtF64) {
         constexpr int V = DT == kDtF32 ? 4 : 8;
-        cols_vec = cols && (uintptr_t)x % 16 == 0 && g.kshape[g.nk - 1] % V == 0;
-        for (int d = 0; d + 1 < g.nk; ++d) cols_vec = cols_vec && g.kst[d] % V == 0;
-        for (int d = 0; d < g.nr; ++d) cols_vec = cols_vec && g.rst[d] % V == 0;
+        pl.cols_vec = pl.cols && (uintptr_t)x % 16 == 0 && g.kshape[g.nk - 1] % V == 0;
+        for (int d = 0; d + 1 < g.nk; ++d) pl.cols_vec = pl.cols_vec && g.kst[d] % V == 0;
+        for (int d = 0; d < g.nr; ++d) pl.cols_vec = pl.cols_vec && g.rst[d] % V == 0;
     }
     int64_t splits = 1;
-    if (rows) {
+    if (pl.rows) {
         splits = 2048 / g.n_out;  // (8192 blocks for one output measured slower: 0.057 vs 0.051 ms)
         const int64_t cap = g.n_red / 4096;  // >= 4096 elements per block
         if (splits > cap) splits = cap;
-    } else if (cols) {
+    } else if (pl.cols) {
         // ~2048 blocks of 256 threads: a streaming pass needs the waves (the
         // [8192, 8192] f32 column sum ran 58 % of HBM peak with 512 blocks,
         // 63-65 % with 2048)
-        const int64_t per_block = cols_vec ? 256 * (DT == kDtF32 ? 4 : 8) : 256;
+        const int64_t per_block = pl.cols_vec ? 256 * (DT == kDtF32 ? 4 : 8) : 256;
         const int64_t col_blocks = (g.n_out + per_block - 1) / per_block;
         splits = 2048 / col_blocks;
         const int64_t cap = g.n_red / 32;  // >= 32 reduced elements per thread
         if (splits > cap) splits = cap;
-    } else {
+    }
+    pl.splits = splits < 1 ? 1 : splits;
+    return pl;
+}
+
+// ws_ext: a caller-provided workspace of at least the plan's size (the
+// static scratch of oxm_reduce_noalloc), or nullptr to allocate one on the
+// stream.
+template <int DT, int OP>
+hipError_t red_launch(const RedGeom &g, const void *x, void *out, hipStream_t st, void *ws_ext) {
+    using A = typename El<DT>::Acc;
+    if (g.n_out == 0) return hipSuccess;
+    const RedPlan pl = plan_reduce<DT>(g, x);
+    const bool rows = pl.rows, cols = pl.cols, cols_vec = pl.cols_vec;
+    const int64_t splits = pl.splits;
+    if (!rows && !cols) {
         hipLaunchKernelGGL((reduce_per_thread<DT, OP>), dim3(grid_for(g.n_out)), dim3(256), 0, st, g, x, out);
         return hipGetLastError();
     }
-    if (splits < 1) splits = 1;
     A *ws = nullptr;
+    bool owned = false;
     hipError_t e;
-    if (splits > 1 && (e = hipMallocAsync((void **)&ws, sizeof(A) * g.n_out * splits, st)) != hipSuccess) return e;
+    if (splits > 1) {
+        if (ws_ext) {
+            ws = (A *)ws_ext;
+        } else {
+            if ((e = hipMallocAsync((void **)&ws, sizeof(A) * g.n_out * splits, st)) != hipSuccess) return e;
+            owned = true;
+        }
+    }
     auto finish = [&](int64_t stride_o, int64_t stride_s) {
         if (g.n_out <= 1024 && splits >= 64)
             hipLaunchKernelGGL((reduce_finish_block<DT, OP>), dim3((unsigned)g.n_out), dim3(256), 0, st, ws, (int)splits,
@@ -900,7 +931,7 @@ hipError_t red_launch(const RedGeom &g, const void *x, void *out, hipStream_t st
                                ws, g.n_out, (int)splits, out);
     }
     e = hipGetLastError();
-    if (ws) {
+    if (owned) {
         hipError_t f = hipFreeAsync(ws, st);
         if (e == hipSuccess) e = f;
     }
@@ -908,8 +939,15 @@ hipError_t red_launch(const RedGeom &g, const void *x, void *out, hipStream_t st
 }
 
 template <int DT>
-hipError_t red_dispatch(int op, const RedGeom &g, const void *x, void *out, hipStream_t st) {
-    return op == kRedSum ? red_launch<DT, kRedSum>(g, x, out, st) : red_launch<DT, kRedMax>(g, x, out, st);
+hipError_t red_dispatch(int op, const RedGeom &g, const void *x, void *out, hipStream_t st, void *ws) {
+    return op == kRedSum ? red_launch<DT, kRedSum>(g, x, out, st, ws) : red_launch<DT, kRedMax>(g, x, out, st, ws);
+}
+
+template <int DT>
+size_t ws_bytes(const RedGeom &g, const void *x) {
+    if (g.n_out == 0) return 0;
+    const RedPlan pl = plan_reduce<DT>(g, x);
+    return (pl.rows || pl.cols) && pl.splits > 1 ? sizeof(typename El<DT>::Acc) * g.n_out * pl.splits : 0;
 }
 
 }  // namespace
@@ -1046,13 +1084,52 @@ hipError_t launch_sgd(int pdt, int gdt, int64_t n, void *p, const void *g, float
                          : sgd_typed<kDtF16, kDtF16>(n, p, g, v, lr, momentum, weight_decay, nesterov, st);
 }
 
-hipError_t launch_reduce(int dtype, int op, const RedGeom &g, const void *x, void *out, hipStream_t st) {
+hipError_t launch_reduce(int dtype, int op, const RedGeom &g, const void *x, void *out, hipStream_t st, void *ws) {
     switch (dtype) {
-    case kDtF32: return red_dispatch<kDtF32>(op, g, x, out, st);
-    case kDtBF16: return red_dispatch<kDtBF16>(op, g, x, out, st);
-    case kDtF16: return red_dispatch<kDtF16>(op, g, x, out, st);
-    default: return red_dispatch<kDtF64>(op, g, x, out, st);
+    case kDtF32: return red_dispatch<kDtF32>(op, g, x, out, st, ws);
+    case kDtBF16: return red_dispatch<kDtBF16>(op, g, x, out, st, ws);
+    case kDtF16: return red_dispatch<kDtF16>(op, g, x, out, st, ws);
+    default: return red_dispatch<kDtF64>(op, g, x, out, st, ws);
     }
+}
+
+size_t reduce_workspace_bytes(int dtype, const RedGeom &g, const void *x) {
+    switch (dtype) {
+    case kDtF32: return ws_bytes<kDtF32>(g, x);
+    case kDtBF16: return ws_bytes<kDtBF16>(g, x);
+    case kDtF16: return ws_bytes<kDtF16>(g, x);
+    case kDtF64: return ws_bytes<kDtF64>(g, x);
+    default: return 0;  // integer reductions take no workspace
+    }
+}
+
+// The workspace of oxm_reduce_noalloc: device memory the library owns from
+// load to exit, one copy per GPU, so callers that cannot allocate (graph
+// capture, serving loops) can still split a reduction.  Host code never uses
+// this name as an address (in host code it is only a stand-in for the device
+// symbol): reduce_scratch() looks the device address up with
+// hipGetSymbolAddress once per device and hands that out.
+__device__ __align__(256) unsigned char scratch[kReduceScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxScratchDevices] = {};
+}  // namespace
+
+hipError_t reduce_scratch(void **ptr) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxScratchDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return hipSuccess;
 }
 
 }  // namespace oxm

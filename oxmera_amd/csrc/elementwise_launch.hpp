@@ -48,7 +48,17 @@ hipError_t launch_elementwise(int dtype, int nops, int op, const EwShape &s, voi
 // to a strided destination (operand 0), bits unchanged.
 hipError_t launch_copy(int elem_bytes, const EwShape &s, void *dst, const void *src, bool contig16, hipStream_t st);
 
-hipError_t launch_reduce(int dtype, int op, const RedGeom &g, const void *x, void *out, hipStream_t st);
+// ws: nullptr (a workspace is allocated on the stream when the schedule
+// splits), or a device buffer of at least reduce_workspace_bytes(...).
+hipError_t launch_reduce(int dtype, int op, const RedGeom &g, const void *x, void *out, hipStream_t st,
+                         void *ws = nullptr);
+size_t reduce_workspace_bytes(int dtype, const RedGeom &g, const void *x);
+
+// The static workspace of oxm_reduce_noalloc (elementwise.hip): its size, and
+// its device address on the current device (looked up once per device).
+constexpr size_t kReduceScratchBytes = size_t(8) << 20;
+constexpr int kMaxScratchDevices = 64;
+hipError_t reduce_scratch(void **ptr);
 
 // The same for I32 / I64 / U8 / Bool (elementwise_int.hip): unary neg / abs,
 // binary add / sub / mul / div / eq, reduce sum / max; the host has refused

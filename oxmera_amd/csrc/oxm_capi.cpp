@@ -437,6 +437,9 @@ oxm_status check_out(const oxm_view *out, int dtype, int nd, const int64_t *shap
     return OXM_OK;
 }
 
+oxm_status reduce_impl(int32_t op, const oxm_view *x, const int32_t *axes, int32_t naxes, const oxm_view *out,
+                       void *stream, bool noalloc);
+
 // Integer division with its typed refusal of a zero divisor (BinaryOps::div,
 // crates/oxmera-ops/src/lib.rs:47-48): the kernel raises a device flag,
 // which is read back after the stream has run it, so this call is
@@ -1013,6 +1016,23 @@ oxm_status oxm_reduce_infer(const oxm_view *x, const int32_t *axes, int32_t naxe
 
 oxm_status oxm_reduce(int32_t op, const oxm_view *x, const int32_t *axes, int32_t naxes, const oxm_view *out,
                       void *stream) {
+    return reduce_impl(op, x, axes, naxes, out, stream, false);
+}
+
+oxm_status oxm_reduce_noalloc(int32_t op, const oxm_view *x, const int32_t *axes, int32_t naxes, const oxm_view *out,
+                              void *stream) {
+    return reduce_impl(op, x, axes, naxes, out, stream, true);
+}
+
+}  // extern "C"
+
+namespace {
+
+// oxm_reduce, and with `noalloc` oxm_reduce_noalloc: the same validation and
+// kernels; the split partials go to the library's static per-device scratch
+// instead of a stream allocation.
+oxm_status reduce_impl(int32_t op, const oxm_view *x, const int32_t *axes, int32_t naxes, const oxm_view *out,
+                       void *stream, bool noalloc) {
     if (op != OXM_RED_SUM && op != OXM_RED_MAX) return fail(OXM_E_INVALID_ARGUMENT, "reduce: unknown op %d", op);
     const char *name = op == OXM_RED_SUM ? "sum" : "max";
     oxm_status st;
@@ -1072,14 +1092,34 @@ oxm_status oxm_reduce(int32_t op, const oxm_view *x, const int32_t *axes, int32_
     }
     const int es = dtype_size(x->dtype);
     hipStream_t s = (hipStream_t)stream;
-    hipError_t e = is_int_dtype(x->dtype)
-                       ? oxm::launch_reduce_int(x->dtype, op, g, (const char *)x->data + x->offset * es,
-                                                (char *)out->data + out->offset * es, s)
-                       : oxm::launch_reduce(x->dtype, op, g, (const char *)x->data + x->offset * es,
-                                            (char *)out->data + out->offset * es, s);
+    const char *px = (const char *)x->data + x->offset * es;
+    char *po = (char *)out->data + out->offset * es;
+    if (is_int_dtype(x->dtype)) {  // no workspace either way
+        hipError_t e = oxm::launch_reduce_int(x->dtype, op, g, px, po, s);
+        if (e != hipSuccess) return hip_fail(e, name);
+        return finish(s, name);
+    }
+    void *ws = nullptr;
+    if (noalloc) {
+        const size_t need = oxm::reduce_workspace_bytes(x->dtype, g, px);
+        if (need > oxm::kReduceScratchBytes)
+            return fail(OXM_E_NOT_IMPLEMENTED,
+                        "%s (no-allocation variant) is not implemented for a reduction whose split partials need "
+                        "%zu bytes: the static scratch holds %zu",
+                        name, need, oxm::kReduceScratchBytes);
+        if (need > 0) {
+            hipError_t e = oxm::reduce_scratch(&ws);
+            if (e != hipSuccess) return hip_fail(e, name);
+        }
+    }
+    hipError_t e = oxm::launch_reduce(x->dtype, op, g, px, po, s, ws);
     if (e != hipSuccess) return hip_fail(e, name);
     return finish(s, name);
 }
+
+}  // namespace
+
+extern "C" {
 
 oxm_status oxm_copy_view(const oxm_view *src, const oxm_view *dst, void *stream) {
     const char *op = "contiguous";
