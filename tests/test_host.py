@@ -342,3 +342,32 @@ def test_epilogue_buffers_are_checked_on_the_host():
         be.matmul(a, b, act=_lib.ACT_GELU, aux=host_tensor([8, 4]).transpose_last())
     with pytest.raises(ox.ShapeMismatch):
         be.matmul(a, b, colsum=host_tensor([4]))
+
+
+# ---- the Rust binding crates (rust/, source only: no cargo in this image) -------------
+
+def test_rust_sys_crate_declares_every_entry_point():
+    """rust/oxmera-hip-sys binds exactly the functions include/oxm.h declares."""
+    src = (ROOT / "rust" / "oxmera-hip-sys" / "src" / "lib.rs").read_text()
+    declared = sorted(set(re.findall(r"pub fn (oxm_[a-z0-9_]+)\s*\(", src)))
+    assert declared == header_functions()
+    # the status codes agree with the header's enum
+    hdr = (ROOT / "include" / "oxm.h").read_text()
+    for name, val in re.findall(r"(OXM_E_[A-Z_]+) = (\d+)", hdr):
+        assert re.search(rf"pub const {name}: oxm_status = {val};", src), name
+
+
+def test_rust_safe_crate_maps_every_status():
+    """oxmera-hip's check() names each Error variant (error.rs:14-102) for its
+    status code."""
+    src = (ROOT / "rust" / "oxmera-hip" / "src" / "lib.rs").read_text()
+    body = src[src.index("fn check("):src.index("// ---- device storage")]
+    for code, variant in [("OXM_E_SHAPE_MISMATCH", "ShapeMismatch"), ("OXM_E_BROADCAST_INCOMPATIBLE",
+                          "BroadcastIncompatible"), ("OXM_E_DTYPE_MISMATCH", "DTypeMismatch"),
+                          ("OXM_E_UNSUPPORTED_DTYPE", "UnsupportedDType"), ("OXM_E_DEVICE_MISMATCH", "DeviceMismatch"),
+                          ("OXM_E_INDEX_OUT_OF_BOUNDS", "IndexOutOfBounds"), ("OXM_E_RANK_MISMATCH", "RankMismatch"),
+                          ("OXM_E_BACKEND_UNAVAILABLE", "BackendUnavailable"),
+                          ("OXM_E_NOT_IMPLEMENTED", "NotImplemented")]:
+        assert re.search(rf"sys::{code} => Err\(Error::{variant}\b", body), code
+    for trait in ("UnaryOps", "BinaryOps", "MatmulOps", "ReduceOps", "Backend"):
+        assert f"impl {trait} for HipBackend" in src, trait
