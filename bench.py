@@ -538,6 +538,30 @@ def extra_line(kind: str, steps: int, warmup: int) -> dict:
     return line
 
 
+def summarize_trace_groups(path: str, kernel: str, skip_frac: float = 0.5) -> dict:
+    """Per (kernel, grid) durations from a rocprofv3 kernel trace of a run
+    that launches several GEMMs per step (the MLP step): each group's
+    dispatches after the first `skip_frac` of them (the warm-up), median and
+    average."""
+    import csv
+    from collections import defaultdict
+    groups = defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        if kernel in r["Kernel_Name"]:
+            nm = r["Kernel_Name"]
+            nm = (nm[:nm.rfind("(")] if nm.endswith(")") else nm).replace("void ", "").replace("oxm::", "").replace(
+                "(anonymous namespace)::", "")
+            groups[(nm, int(r["Grid_Size_X"]))].append(
+                (int(r["Dispatch_Id"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    out = []
+    for (name, grid), v in sorted(groups.items()):
+        v.sort()
+        d = np.array([x[1] for x in v[int(len(v) * skip_frac):]], dtype=np.float64) / 1e6
+        out.append({"kernel": name, "grid_threads": grid, "dispatches": len(v), "used": len(d),
+                    "median_ms": round(float(np.median(d)), 5), "avg_ms": round(float(d.mean()), 5)})
+    return {"groups": out}
+
+
 def summarize_trace(path: str, kernel: str, timed: int, after: int) -> dict:
     """Durations of the launches bench.py timed, from a rocprofv3 kernel trace
     of the same command: the dispatches of the kernel (name containing
@@ -558,6 +582,44 @@ def summarize_trace(path: str, kernel: str, timed: int, after: int) -> dict:
             "span_ms": round((int(win[-1]["End_Timestamp"]) - int(win[0]["Start_Timestamp"])) / 1e6 / timed, 5)}
 
 
+def summarize_pmc(paths: list, copy_bytes: float | None = None) -> dict:
+    """Per-kernel means over the dispatches in rocprofv3 --pmc
+    counter_collection.csv files (one counter pass per file), grouped by
+    kernel name and grid size, with the derived figures the profiles quote:
+    MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 1024
+    SIMDs); LDS bank-conflict share = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE;
+    L2 hit rate = TCC_HIT / (TCC_HIT + TCC_MISS); FETCH_SIZE / WRITE_SIZE
+    (KiB per dispatch) in bytes, FETCH scaled x2 and WRITE x1 -- the factors
+    a plain device copy of known size reads as (bench.py --copy-calibration)."""
+    import csv
+    from collections import defaultdict
+    acc = defaultdict(lambda: defaultdict(list))
+    for path in paths:
+        for r in csv.DictReader(open(path)):
+            name = r["Kernel_Name"]
+            if "oxm::" not in name and "Cijk" not in name:
+                continue
+            short = (name[:name.rfind("(")] if name.endswith(")") else name).replace("void ", "").replace(
+                "oxm::", "").replace("(anonymous namespace)::", "")
+            acc[(short, int(r["Grid_Size"]))][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    out = []
+    for (name, grid), cs in sorted(acc.items()):
+        m = {c: sum(v) / len(v) for c, v in cs.items()}
+        d = {"kernel": name, "grid_threads": grid, "dispatches": max(len(v) for v in cs.values()), "mean": m}
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in m and "GRBM_GUI_ACTIVE" in m:
+            d["mfma_busy"] = round(m["SQ_VALU_MFMA_BUSY_CYCLES"] / (m["GRBM_GUI_ACTIVE"] / 8 * 1024), 4)
+        if "SQ_LDS_BANK_CONFLICT" in m and m.get("SQ_LDS_IDX_ACTIVE"):
+            d["lds_bank_conflict_share"] = round(m["SQ_LDS_BANK_CONFLICT"] / m["SQ_LDS_IDX_ACTIVE"], 4)
+        if "TCC_HIT_sum" in m and "TCC_MISS_sum" in m:
+            d["l2_hit_rate"] = round(m["TCC_HIT_sum"] / (m["TCC_HIT_sum"] + m["TCC_MISS_sum"]), 4)
+        if "FETCH_SIZE" in m:
+            d["fetch_bytes"] = m["FETCH_SIZE"] * 1024 * 2.0
+        if "WRITE_SIZE" in m:
+            d["write_bytes"] = m["WRITE_SIZE"] * 1024 * 1.0
+        out.append(d)
+    return {"kernels": out}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -572,6 +634,10 @@ def main():
     ap.add_argument("--kernel", default="gemm_kernel", help="substring of the kernel name (--summarize-trace)")
     ap.add_argument("--timed", type=int, default=50, help="launches in the timed window (--summarize-trace)")
     ap.add_argument("--after", type=int, default=20, help="launches after the timed window (--summarize-trace)")
+    ap.add_argument("--group", action="store_true",
+                    help="with --summarize-trace: per (kernel, grid) medians over the second half of the run")
+    ap.add_argument("--summarize-pmc", metavar="CSV", nargs="+",
+                    help="summarize rocprofv3 --pmc counter_collection.csv files (one per counter pass) per kernel")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and the extra workload")
     ap.add_argument("--vendor", action="store_true",
                     help="time torch.matmul (the vendor library, hipBLASLt, run as a black box) on the same "
@@ -580,8 +646,14 @@ def main():
                     help="run only a plain 256 MiB device copy (10x), the reference for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE scaling")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        print(json.dumps(summarize_pmc(args.summarize_pmc)), flush=True)
+        return
     if args.summarize_trace:
-        print(json.dumps(summarize_trace(args.summarize_trace, args.kernel, args.timed, args.after)), flush=True)
+        if args.group:
+            print(json.dumps(summarize_trace_groups(args.summarize_trace, args.kernel)), flush=True)
+        else:
+            print(json.dumps(summarize_trace(args.summarize_trace, args.kernel, args.timed, args.after)), flush=True)
         return
     if args.copy_calibration:
         import torch
