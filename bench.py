@@ -479,11 +479,18 @@ def spot_check(kind: str, res, sample, host=None, comp_rows: int = 64):
 
 def kernel_name(kind: str) -> str:
     if kind == "f16":
-        return "gemm_kernel_dl<f16_t,256,256,2,4,2,64> (direct-to-LDS, 2 stages of 64 k, 8 waves)"
+        return "gemm_kernel_dli16<f16_t> (direct-to-LDS, 2 stages of 64 k, 4 waves, 16x16x32 MFMA)"
     if kind == "bf16":
-        return "gemm_kernel_dl<bf16_t,256,256,2,4,2,64> (direct-to-LDS, 2 stages of 64 k, 8 waves)"
+        return "gemm_kernel_dli16<bf16_t> (direct-to-LDS, 2 stages of 64 k, 4 waves, 16x16x32 MFMA)"
     if kind == "f32":
         return "gemm_kernel<float,256,256,2,4,Ld::K,Ld::MN> (register-staged LDS double buffer, 8 waves)"
+    if kind == "c2odd":
+        return ("gemm_kernel<float,256,256,2,4,Ld::KR,Ld::MNR> (rows 0-4095) + gemm_strip<float> (row 4096); "
+                "time per launch covers both")
+    if kind == "c4":
+        return "gemm_kernel<float,128,128,2,2,Ld::K,Ld::MN> (register-staged, 4 waves, 1.5 rounds of tiles)"
+    if kind == "c1":
+        return "gemm_kernel<float,64,64,2,2,Ld::K,Ld::MN> (16 tiles on 16 CUs; launch-latency bound)"
     return "gemm_kernel<float,...> (register-staged; tile chosen by the dispatcher)"
 
 
@@ -533,8 +540,7 @@ def extra_line(kind: str, steps: int, warmup: int) -> dict:
     if kind == "c1":
         line["us_per_launch"] = round(1e3 * r["total_ms"] / steps, 2)
         line["note"] = "launch-latency bound (0.2 us of MFMA work at peak); no roofline target"
-    if kind in ("bf16", "f32", "f16"):
-        line["roofline"] = roofline(kind, r)
+    line["roofline"] = roofline(kind, r)
     return line
 
 

@@ -15,6 +15,7 @@ TileShape tile_shape(int cfg) {
     case kCfgH_256:
     case kCfgH_256_4W:
     case kCfgH_256_1W:
+    case kCfgH_256_1W16:
     case kCfgH_256_NS:
     case kCfgF32_256: return {256, 256};
     case kCfgH_128: return {128, 128};

@@ -53,6 +53,16 @@ hipError_t pick_dli(const GemmArgs &a, int la, int lb, hipStream_t s) {
     return launch_dli<T, true, true>(a, s);
 }
 
+// One wave per SIMD on 16x16x32 MFMAs (K-major operands only).
+template <typename T>
+hipError_t launch_dli16(GemmArgs a, hipStream_t s) {
+    a.group_m = 4;
+    int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n * a.batch;
+    dim3 grid((unsigned)ntiles), block(256);
+    hipLaunchKernelGGL((gemm_kernel_dli16<T>), grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
 template <typename T, int BM, int BN, int WM, int WN, Ld LA>
 hipError_t pick_b(const GemmArgs &a, int lb, hipStream_t s) {
     switch (lb) {

@@ -737,36 +737,71 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// LDS-staged epilogue: each wave writes its WM x WN accumulators one 32-row
-// slab at a time through a padded LDS slab (row stride WN + 8 floats,
-// conflict-free), then stores rows with 16-byte writes, applying the bias and
-// activation (under GELU' the next slab's aux values load while a slab is
-// written).  The caller has drained every DMA into `lds` and synchronised.
-template <int OUT_DT, int WN, int TM, int TN>
-__device__ __forceinline__ void epilogue_slabs(const GemmArgs &p, f32x16_t (&acc)[TM][TN], float *ws, int lane,
-                                               int64_t cbase, int64_t row_base, int64_t col0, const float (&b4)[4],
-                                               float (&cs)[4]) {
+// f(integral_constant<I>), f(integral_constant<I + 1>), ..., f(integral_constant<N - 1>).
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+// Writes 32-row slab I of a wave's accumulators into the LDS slab ws (f32
+// [32][WN + 8]).  32x32 blocks (f32x16_t): lane l holds column l % 32 of rows
+// 8 (e / 4) + 4 (l / 32) + e % 4 of block row I.  16x16 blocks (f32x4_t):
+// lane l holds column l % 16 of rows 4 (l / 16) + e; the slab is block rows
+// 2I and 2I + 1.
+template <int I, int WN, int TM, int TN>
+__device__ __forceinline__ void fill_slab(float *ws, f32x16_t (&acc)[TM][TN], int lane) {
     constexpr int kSld = WN + 8;
     const int half = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            ws[(8 * (e >> 2) + 4 * half + (e & 3)) * kSld + j * 32 + (lane & 31)] = acc[I][j][e];
+}
+template <int I, int WN, int TM, int TN>
+__device__ __forceinline__ void fill_slab(float *ws, f32x4_t (&acc)[TM][TN], int lane) {
+    constexpr int kSld = WN + 8;
+    const int q = lane >> 4;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ws[(16 * h + 4 * q + e) * kSld + j * 16 + (lane & 15)] = acc[2 * I + h][j][e];
+}
+
+// 32-row slabs in a wave tile of TM block rows.
+template <typename Acc, int TM>
+constexpr int kSlabs = std::is_same<Acc, f32x16_t>::value ? TM : TM / 2;
+
+// LDS-staged epilogue: each wave writes its WM x WN accumulators one 32-row
+// slab at a time through a padded LDS slab (row stride WN + 8 floats), then
+// stores rows with 16-byte writes, applying the bias and activation (under
+// GELU' the next slab's aux values load while a slab is written).  The caller
+// has drained every DMA into `lds` and synchronised.
+template <int OUT_DT, int WN, typename Acc, int TM, int TN>
+__device__ __forceinline__ void epilogue_slabs(const GemmArgs &p, Acc (&acc)[TM][TN], float *ws, int lane,
+                                               int64_t cbase, int64_t row_base, int64_t col0, const float (&b4)[4],
+                                               float (&cs)[4]) {
+    constexpr int NSLAB = kSlabs<Acc, TM>;
     // GELU' with 16-bit output and 64-column wave tiles: every slab's aux
     // values (64 VGPRs at most) load before the first store; otherwise
     // write_slab loads them per row
     constexpr bool kPre = OUT_DT != kDtF32 && WN <= 64;
     const bool pre_ok = kPre && p.act == kActDGelu && slab_aligned(p);
-    AuxSlab<OUT_DT, WN> pre[kPre ? TM : 1];
+    AuxSlab<OUT_DT, WN> pre[kPre ? NSLAB : 1];
     if constexpr (kPre) {
         if (pre_ok) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i) load_aux_slab<OUT_DT, WN>(p, cbase, row_base + i * 32, col0, lane, pre[i]);
+            for (int i = 0; i < NSLAB; ++i) load_aux_slab<OUT_DT, WN>(p, cbase, row_base + i * 32, col0, lane, pre[i]);
         }
     }
-    static_for<0, TM>([&](auto ic) {
+    static_for<0, NSLAB>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-                ws[(8 * (e >> 2) + 4 * half + (e & 3)) * kSld + j * 32 + (lane & 31)] = acc[i][j][e];
+        fill_slab<i, WN>(ws, acc, lane);
         wave_sync();
         const int64_t row0 = row_base + i * 32;
         if (pre_ok)
@@ -777,8 +812,8 @@ __device__ __forceinline__ void epilogue_slabs(const GemmArgs &p, f32x16_t (&acc
     });
 }
 
-template <int NT, int WM, int WN, int TM, int TN, int LDS_BYTES>
-__device__ __forceinline__ void epilogue_lds(const GemmArgs &p, f32x16_t (&acc)[TM][TN], uint8_t *lds, int wave,
+template <int NT, int WM, int WN, int TM, int TN, int LDS_BYTES, typename Acc>
+__device__ __forceinline__ void epilogue_lds(const GemmArgs &p, Acc (&acc)[TM][TN], uint8_t *lds, int wave,
                                              int lane, int64_t cbase, int64_t row_base, int64_t col0) {
     constexpr int kSld = WN + 8;
     static_assert(NT / 64 * 32 * kSld * 4 <= LDS_BYTES, "epilogue staging must fit in LDS");
@@ -801,14 +836,6 @@ __device__ __forceinline__ void epilogue_lds(const GemmArgs &p, f32x16_t (&acc)[
 }
 
 // ---- the kernel -------------------------------------------------------------
-
-template <int I, int N, typename F>
-__device__ __forceinline__ void static_for(F &&f) {
-    if constexpr (I < N) {
-        f(std::integral_constant<int, I>{});
-        static_for<I + 1, N>(f);
-    }
-}
 
 template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, Ld LA, Ld LB, bool SCHED = true, int PF = 1>
 __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel(GemmArgs p) {
@@ -1490,6 +1517,175 @@ __global__ void __launch_bounds__(256) gemm_kernel_dli(GemmArgs p) {
         const typename LA::Stage sta = la.prep(lds, 0);
         const typename LB::Stage stb = lb.prep(lds + kStageA, 0);
         group(I1{}, YES{}, INone{}, INone{}, lds, sta, stb);  // group 3 of the last step
+    }
+    // drain every DMA (the last steps' are out of range) before the LDS is reused
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();
+    epilogue_lds<NT, WM, WN, TM, TN, 2 * kStage>(p, acc, lds, wave, lane, tc.bidx * p.M * p.N, m0 + wm * WM,
+                                                 n0 + wn * WN);
+}
+
+// ---- one wave per SIMD on 16x16x32 MFMAs ------------------------------------
+
+// bf16 / f16 on v_mfma_f32_16x16x32_{bf16,f16}: a 16-byte fragment holds the
+// 8 k values one lane contributes (lane l: row l % 16, k 8 (l / 16) .. +7 of
+// the 32), identically for A and B; the 4 accumulators of lane l are column
+// l % 16 of rows 4 (l / 16) .. +3.
+template <typename T>
+struct Mma16;
+template <>
+struct Mma16<bf16_t> {
+    __device__ __forceinline__ static void run(f32x4_t &acc, const uint4 &a, const uint4 &b) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                      acc, 0, 0, 0);
+    }
+};
+template <>
+struct Mma16<f16_t> {
+    __device__ __forceinline__ static void run(f32x4_t &acc, const uint4 &a, const uint4 &b) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                     acc, 0, 0, 0);
+    }
+};
+
+// 16x16x32 fragments of a K-major operand from a BKS = 64 stage (lds_off
+// layout): tile I is rows row0 + 16 I .. +15, group g is k 32 g .. +31; lane l
+// reads row l % 16 at 16-byte chunk 4 g + l / 16.  Sixteen rows of one chunk
+// fall in sixteen distinct bank groups, and rows r and r + 16 differ by 8 row
+// pairs (2048 bytes) with the same swizzle.
+struct FragReader16 {
+    uint32_t off[2];
+    __device__ __forceinline__ FragReader16(uint32_t region, int row0, int lane) {
+        const int r = row0 + (lane & 15);
+#pragma unroll
+        for (int g = 0; g < 2; ++g) off[g] = region + lds_off(r, 4 * g + (lane >> 4));
+    }
+    template <int I>
+    __device__ __forceinline__ uint4 read1(const uint8_t *stage, int g) const {
+        return *(const uint4 *)(stage + off[g] + I * 2048);
+    }
+};
+
+// 256x256 tile, 2x2 waves of 128x128, one wave per SIMD, K-major 16-bit
+// operands, 16x16x32 MFMAs (OXM_GEMM_CFG=7).  Against the 32x32x16 kernels a
+// 16x16x32 MFMA is half as long, so each fragment read and DMA instruction
+// of the hand-placed stream has twice as many MFMA slots to hide in: a
+// 64-k stage is two groups of 64 MFMA slots (8 x 8 blocks); slot 2r of a
+// group reads fragment r of the next group (A0, B0 .. B7, A1 .. A7, the order
+// its MFMAs consume them) and the stage's 16 DMA instructions take every
+// fourth slot from slot 8 of the step (placements swept: DMA offset 0 / 8 /
+// 16 / 24 / 40 / 64 slots, spacing 2 / 3 / 4 / 6 / 7 / 8, fragment-read
+// spacing 1 / 2 / 3, per-wave DMA offsets; this one measured best).  The
+// second group of each stage is deferred past the barrier.  The MFMA sums
+// equal those of the 32x32x16 kernels bit for bit on the shapes tested.
+template <typename T, int DF = 8, int DS = 4, int RS = 2>
+__global__ void __launch_bounds__(256) gemm_kernel_dli16(GemmArgs p) {
+    constexpr int BM = 256, BN = 256, BKS = 64, NT = 256, WAVES_N = 2;
+    constexpr int WM = 128, WN = 128, TM = 8, TN = 8;  // 16x16 blocks per wave
+    constexpr int kStageA = BM * BKS * 2, kStageB = BN * BKS * 2;
+    constexpr int kStage = kStageA + kStageB;
+    static_assert(Elem<T>::kBytes == 2, "direct-to-LDS path is for 16-bit operands");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStage];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const TileCoord tc = tile_coord<BM, BN>(p, blockIdx.x);
+    const int64_t m0 = tc.m0, n0 = tc.n0;
+    using LA = DirectLoader<BM, NT, false, BKS>;
+    using LB = DirectLoader<BN, NT, false, BKS>;
+    LA la((const char *)p.a + (tc.offa + m0 * p.sam) * 2, p.sam, p.sak, p.M - m0, p.K, wave, lane);
+    LB lb((const char *)p.b + (tc.offb + n0 * p.sbn) * 2, p.sbn, p.sbk, p.N - n0, p.K, wave, lane);
+    constexpr int L = LA::kPer + LB::kPer;  // DMA instructions per wave per stage
+    constexpr int Q = TM * TN;              // MFMA slots per group
+    constexpr int R = TM + TN;              // fragment reads per group
+    static_assert(DF + (L - 1) * DS < 2 * Q, "DMA must fit the slots of one stage");
+    static_assert((R - 1) * RS < Q, "fragment reads must fit the slots of one group");
+    const FragReader16 fra(0, wm * WM, lane);
+    const FragReader16 frb(kStageA, wn * WN, lane);
+
+    f32x4_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{};
+    uint4 fa[2][TM], fb[2][TN];
+
+    // One group (GI-th of a stage; GI < 0: no DMA): the MFMAs of register set
+    // USE (MF = false: none); fragment reads of group GN (GN < 0: none) of
+    // stage `rs` into set USE ^ 1; DMA instruction l of the next stage in
+    // stage slot DF + l * DS.
+    auto group = [&](auto usec, auto mfc, auto gnc, auto gic, const uint8_t *rs, const typename LA::Stage &sta,
+                     const typename LB::Stage &stb) {
+        constexpr int USE = decltype(usec)::value, GN = decltype(gnc)::value, GI = decltype(gic)::value;
+        constexpr bool MF = decltype(mfc)::value;
+        static_for<0, Q>([&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            if constexpr (MF) Mma16<T>::run(acc[q / TN][q % TN], fa[USE][q / TN], fb[USE][q % TN]);
+            if constexpr (GN >= 0 && q % RS == 0 && q / RS < R) {
+                constexpr int r = q / RS;
+                if constexpr (r == 0)
+                    fa[USE ^ 1][0] = fra.template read1<0>(rs, GN);
+                else if constexpr (r <= TN)
+                    fb[USE ^ 1][r - 1] = frb.template read1<(r >= 1 && r <= TN ? r - 1 : 0)>(rs, GN);
+                else
+                    fa[USE ^ 1][r - TN] = fra.template read1<(r > TN ? r - TN : 0)>(rs, GN);
+            }
+            constexpr int sg = GI * Q + q;
+            if constexpr (GI >= 0 && sg >= DF && (sg - DF) % DS == 0 && (sg - DF) / DS < L) {
+                constexpr int l = (sg - DF) / DS;
+                if constexpr (l < LA::kPer)
+                    la.template issue_one<(l < LA::kPer ? l : 0)>(sta, wave);
+                else
+                    lb.template issue_one<(l >= LA::kPer ? l - LA::kPer : 0)>(stb, wave);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using INone = std::integral_constant<int, -1>;
+    using YES = std::integral_constant<bool, true>;
+    using NO = std::integral_constant<bool, false>;
+    // every LDS read of this wave landed; its DMA into the next stage landed;
+    // then all waves
+    auto stage_barrier = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & ~(0xF << 8));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    const int nk = (int)((p.K + BKS - 1) / BKS);
+    // Prologue: DMA of steps 0 and 1, wait for step 0, its group-0 fragments.
+    la.issue(lds, 0, wave);
+    lb.issue(lds + kStageA, 0, wave);
+    la.issue(lds + kStage, 1, wave);
+    lb.issue(lds + kStage + kStageA, 1, wave);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(L));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        const typename LA::Stage sta = la.prep(lds, 0);
+        const typename LB::Stage stb = lb.prep(lds + kStageA, 0);
+        group(I1{}, NO{}, I0{}, INone{}, lds, sta, stb);
+        group(I0{}, YES{}, I1{}, INone{}, lds, sta, stb);
+    }
+    for (int kt = 1; kt < nk; ++kt) {
+        stage_barrier();
+        const uint8_t *stage = lds + (kt & 1) * kStage;
+        uint8_t *other = lds + ((kt & 1) ^ 1) * kStage;
+        // DMA of step kt+1 into the stage step kt-1 used (past K: zeros)
+        const typename LA::Stage sta = la.prep(other, kt + 1);
+        const typename LB::Stage stb = lb.prep(other + kStageA, kt + 1);
+        group(I1{}, YES{}, I0{}, I0{}, stage, sta, stb);  // group 1 of step kt-1
+        group(I0{}, YES{}, I1{}, I1{}, stage, sta, stb);  // group 0 of step kt
+    }
+    {
+        const typename LA::Stage sta = la.prep(lds, 0);
+        const typename LB::Stage stb = lb.prep(lds + kStageA, 0);
+        group(I1{}, YES{}, INone{}, INone{}, lds, sta, stb);  // group 1 of the last step
     }
     // drain every DMA (the last steps' are out of range) before the LDS is reused
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));

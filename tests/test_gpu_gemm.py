@@ -121,8 +121,9 @@ def test_layouts_full(hip, dtype, la, lb):
 # ragged edge tiles in M and N and a K tail: 1 = 256x256 direct-to-LDS, 2x4
 # waves (the default for large problems); 3 = the same with 2x2 waves; 4 =
 # 256x256 register-staged; 6 = 256x256 direct-to-LDS with one wave per SIMD
-# and a hand-placed instruction stream; 2 = 128x128.
-TILE_CFGS = {"256": 1, "256_4w": 3, "256_regstaged": 4, "256_1w": 6, "128": 2}
+# and a hand-placed instruction stream; 7 = the same on 16x16x32 MFMAs (both
+# operands K-major; other layouts take 6); 2 = 128x128.
+TILE_CFGS = {"256": 1, "256_4w": 3, "256_regstaged": 4, "256_1w": 6, "256_1w16": 7, "128": 2}
 EDGE_SHAPES = [(300, 200, 264), (264, 136, 520), (64, 72, 64), (520, 64, 8)]
 
 
@@ -269,10 +270,11 @@ def test_zero_sized_and_k_zero(hip):
 
 # ---- epilogues --------------------------------------------------------------------
 
-# cfg: None = the dispatcher's choice; "1" / "6" force the 256x256 2x4-wave and
-# one-wave-per-SIMD 16-bit kernels (OXM_GEMM_CFG), whose epilogues differ in
-# wave tile (128x64 / 128x128)
-EPI_CFGS = [None, "1", "6"]
+# cfg: None = the dispatcher's choice; "1" / "6" / "7" force the 256x256
+# 2x4-wave and the two one-wave-per-SIMD 16-bit kernels (OXM_GEMM_CFG), whose
+# epilogues differ in wave tile (128x64 / 128x128) and accumulator layout
+# (32x32 / 16x16 blocks)
+EPI_CFGS = [None, "1", "6", "7"]
 
 
 def _force_cfg(monkeypatch, cfg):
@@ -280,7 +282,7 @@ def _force_cfg(monkeypatch, cfg):
         monkeypatch.setenv("OXM_GEMM_CFG", cfg)
 
 
-@pytest.mark.parametrize("cfg", EPI_CFGS, ids=["auto", "cfg1", "cfg6"])
+@pytest.mark.parametrize("cfg", EPI_CFGS, ids=["auto", "cfg1", "cfg6", "cfg7"])
 @pytest.mark.parametrize("dtype,out", [(F32, F32), (BF16, F32), (BF16, BF16), (F16, F16)],
                          ids=["f32", "bf16-f32", "bf16-bf16", "f16-f16"])
 def test_bias_gelu_epilogue(hip, monkeypatch, dtype, out, cfg):
@@ -335,7 +337,7 @@ def test_gelu_accuracy(hip):
     assert np.isnan(nan).all()
 
 
-@pytest.mark.parametrize("cfg", EPI_CFGS, ids=["auto", "cfg1", "cfg6"])
+@pytest.mark.parametrize("cfg", EPI_CFGS, ids=["auto", "cfg1", "cfg6", "cfg7"])
 @pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
 def test_dgelu_epilogue(hip, monkeypatch, dtype, cfg):
     _force_cfg(monkeypatch, cfg)
@@ -365,7 +367,7 @@ def _check_colsum(cs: ox.Tensor, out: np.ndarray, what: str):
     assert worst <= 1.0, f"{what}: column sum off by {worst:.3g} x the f32 summation bound"
 
 
-@pytest.mark.parametrize("cfg", EPI_CFGS, ids=["auto", "cfg1", "cfg6"])
+@pytest.mark.parametrize("cfg", EPI_CFGS, ids=["auto", "cfg1", "cfg6", "cfg7"])
 @pytest.mark.parametrize("case", ["f32", "f32_ragged", "bf16_dgelu", "bf16_gelu_bf16out", "f32_batched",
                                   "bf16_256tiles"])
 def test_epilogue_column_sums(hip, monkeypatch, case, cfg):

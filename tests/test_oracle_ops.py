@@ -199,7 +199,7 @@ def test_int_reductions_closed_forms():
     assert int(R.int_reduce(x, [], 0, R.I32)) == want
     perm = np.random.default_rng(0).permutation(n).astype(np.int32).reshape(250, 400)
     assert int(R.int_reduce(perm, [], 0, R.I32)) == want
-    np.testing.assert_array_equal(R.int_reduce(x, [1], 0, R.I64 if False else R.I32),
+    np.testing.assert_array_equal(R.int_reduce(x, [1], 0, R.I32),
                                   (400 * np.arange(250, dtype=np.int64) * 400 + 400 * 399 // 2).astype(np.int32))
     # max is the last of a sorted copy; Bool sum / max are any()
     y = np.random.default_rng(1).integers(-50, 50, (7, 9)).astype(np.int64)
