@@ -5,6 +5,7 @@ Configurations from the north star (BASELINE.json "configs"):
   C2  f32 4096^3 N(0,1); odd 4097 x 4095 x 4093     -> checked in full + checksums
   C3  bf16 8192^3, B a transposed view [1, 8192]    -> >= 256 seeded rows x all 8192
                                                        columns + full checksums
+      (and the same shape and layout with f16 operands)
   C4  f32 batched: A every other row of [32,1024,1024], B [1,1024,768] broadcast
                                                     -> checked in full + per-batch checksums
 plus every operand layout the loaders distinguish (K-contiguous, M/N-contiguous,
@@ -497,6 +498,22 @@ def test_c3_bf16_8192_nt(hip):
     log(f"C3: oracle over {len(rows)} rows x all {n} columns")
     check_rows(c, a, b, rows, BF16, n, "C3 rows")
     check_checksums(c, a, b, n, "C3")
+
+
+def test_c3_f16_8192_nt(hip):
+    """configs[2]'s shape and layout with f16 operands (the bench's f16 line;
+    the 16x16x32 one-wave kernel's f16 instantiation by default)."""
+    n = 8192
+    rng = np.random.default_rng(33)
+    log("C3 f16 8192^3, B transposed view")
+    a = Operand(F16, host_buffer(F16, rng.normal(0, 0.02, n * n).astype(np.float32)), (n, n), (n, 1))
+    b = Operand(F16, host_buffer(F16, rng.normal(0, 0.02, n * n).astype(np.float32)), (n, n), (1, n))
+    c = hip.matmul(a.dev, b.dev, out_dtype=F32)
+    rows = sample_rows(n, 256, 7)
+    assert len(rows) >= 256
+    log(f"C3 f16: oracle over {len(rows)} rows x all {n} columns")
+    check_rows(c, a, b, rows, F16, n, "C3 f16 rows")
+    check_checksums(c, a, b, n, "C3 f16")
 
 
 def test_c4_batched_broadcast(hip):
