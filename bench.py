@@ -479,9 +479,9 @@ def spot_check(kind: str, res, sample, host=None, comp_rows: int = 64):
 
 def kernel_name(kind: str) -> str:
     if kind == "f16":
-        return "gemm_kernel_dli16<f16_t> (direct-to-LDS, 2 stages of 64 k, 4 waves, 16x16x32 MFMA)"
+        return "gemm_kernel_dli16<f16_t, true> (global_load_lds DMA, 2 stages of 64 k, 4 waves, 16x16x32 MFMA)"
     if kind == "bf16":
-        return "gemm_kernel_dli16<bf16_t> (direct-to-LDS, 2 stages of 64 k, 4 waves, 16x16x32 MFMA)"
+        return "gemm_kernel_dli16<bf16_t, true> (global_load_lds DMA, 2 stages of 64 k, 4 waves, 16x16x32 MFMA)"
     if kind == "f32":
         return "gemm_kernel<float,256,256,2,4,Ld::K,Ld::MN> (register-staged LDS double buffer, 8 waves)"
     if kind == "c2odd":

@@ -1,6 +1,8 @@
 // gemm.hip -- tile-shape table and dtype dispatch of the GEMM kernels.
 // The instantiations live in one translation unit per dtype
 // (gemm_f32.hip, gemm_bf16.hip, gemm_f16.hip) so they build in parallel.
+#include <cstdlib>
+
 #include "gemm_launch.hpp"
 #include "gemm_kernels.hpp"
 
@@ -9,6 +11,12 @@ namespace oxm {
 hipError_t launch_gemm_f32(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipStream_t s);
 hipError_t launch_gemm_bf16(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipStream_t s);
 hipError_t launch_gemm_f16(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipStream_t s);
+
+bool use_global_dma(const GemmArgs &a) {
+    if (a.K < 64 || a.K % 64 != 0) return false;
+    const char *v = getenv("OXM_GEMM_GLOBAL_DMA");
+    return !(v && v[0] == '0');
+}
 
 TileShape tile_shape(int cfg) {
     switch (cfg) {

@@ -13,18 +13,35 @@ hipError_t launch_one(const GemmArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Whether the direct-to-LDS kernels may issue their DMA through
+// global_load_lds_dwordx4 (DirectLoader GLB): K a whole number of 64-k
+// stages, and not switched off with OXM_GEMM_GLOBAL_DMA=0 (read at each
+// call, like OXM_GEMM_CFG).
+bool use_global_dma(const GemmArgs &a);
+
 // Direct-to-LDS kernel (16-bit operands, each K- or M/N-contiguous).
-template <typename T, int BM, int BN, int WM, int WN, int NS, int BKS, bool AMN, bool BMN>
+template <typename T, int BM, int BN, int WM, int WN, int NS, int BKS, bool AMN, bool BMN, bool GLB = false>
 hipError_t launch_dl(GemmArgs a, hipStream_t s) {
     a.group_m = 4;
     int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n * a.batch;
     dim3 grid((unsigned)ntiles), block(WM * WN * 64);
-    hipLaunchKernelGGL((gemm_kernel_dl<T, BM, BN, WM, WN, NS, BKS, AMN, BMN>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((gemm_kernel_dl<T, BM, BN, WM, WN, NS, BKS, AMN, BMN, GLB>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int NS, int BKS>
+// GLB: also instantiate the global_load_lds variant and take it when
+// use_global_dma allows (the default configurations).
+template <typename T, int BM, int BN, int WM, int WN, int NS, int BKS, bool GLB = false>
 hipError_t pick_dl(const GemmArgs &a, int la, int lb, hipStream_t s) {
+    if constexpr (GLB) {
+        static_assert(BKS == 64, "global DMA with 64-k stages");
+        if (use_global_dma(a)) {
+            if (la == kLdK && lb == kLdK) return launch_dl<T, BM, BN, WM, WN, NS, BKS, false, false, true>(a, s);
+            if (la == kLdK) return launch_dl<T, BM, BN, WM, WN, NS, BKS, false, true, true>(a, s);
+            if (lb == kLdK) return launch_dl<T, BM, BN, WM, WN, NS, BKS, true, false, true>(a, s);
+            return launch_dl<T, BM, BN, WM, WN, NS, BKS, true, true, true>(a, s);
+        }
+    }
     if (la == kLdK && lb == kLdK) return launch_dl<T, BM, BN, WM, WN, NS, BKS, false, false>(a, s);
     if (la == kLdK) return launch_dl<T, BM, BN, WM, WN, NS, BKS, false, true>(a, s);
     if (lb == kLdK) return launch_dl<T, BM, BN, WM, WN, NS, BKS, true, false>(a, s);
@@ -59,7 +76,10 @@ hipError_t launch_dli16(GemmArgs a, hipStream_t s) {
     a.group_m = 4;
     int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n * a.batch;
     dim3 grid((unsigned)ntiles), block(256);
-    hipLaunchKernelGGL((gemm_kernel_dli16<T>), grid, block, 0, s, a);
+    if (use_global_dma(a))
+        hipLaunchKernelGGL((gemm_kernel_dli16<T, true>), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((gemm_kernel_dli16<T, false>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 

@@ -1033,7 +1033,17 @@ constexpr int waitcnt_vm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | (
 // the stage layout is produced by the choice of global addresses.  With
 // BKS = 64 a K-major row is 128 bytes and every row is one 128-byte request
 // (BKS = 32 halves the bytes per L2 request).
-template <int ROWS, int NT, bool MN, int BKS>
+//
+// GLB: the DMA goes through global_load_lds_dwordx4 (64-bit base + 32-bit
+// lane offset) instead of buffer_load_dwordx4 ... lds: the same data
+// movement, but its issue stalls the wave about half as long (8192^3 bf16 on
+// the one-wave kernel: 2554 against 2850 cycles per 64-k stage).  It has no
+// range check, so it serves only K a multiple of BKS (no partial chunk to
+// zero): rows (K-major) or 8-element column chunks (M/N-major) past the
+// operand's edge read the last valid ones instead -- they feed only outputs
+// past M or N, which are never stored -- and steps past K re-read the last
+// step into a stage that is never consumed.
+template <int ROWS, int NT, bool MN, int BKS, bool GLB = false>
 struct DirectLoader {
     static constexpr int kWaves = NT / 64;
     static constexpr int kBlocks = ROWS * BKS * 2 / 1024;
@@ -1069,7 +1079,12 @@ struct DirectLoader {
                     r = 2 * sr + (h ^ ((sr >> 2) & 1));
                     chunk = pc ^ (sr & 7);
                 }
-                voff[i] = r < rows_left ? (uint32_t)(r * s_mn * 2 + chunk * 16) : kOob;
+                if constexpr (GLB) {
+                    const int64_t rc = r < rows_left ? r : rows_left - 1;
+                    voff[i] = (uint32_t)(rc * s_mn * 2 + chunk * 16);
+                } else {
+                    voff[i] = r < rows_left ? (uint32_t)(r * s_mn * 2 + chunk * 16) : kOob;
+                }
                 krow[i] = 0;
             }
         } else {
@@ -1085,11 +1100,18 @@ struct DirectLoader {
                 const int r = pos / (ROWS * 2), bir = pos % (ROWS * 2);
                 const int mn = (((bir >> 6) ^ (r & 3)) << 5) + ((bir & 63) >> 1);
                 krow[i] = r;
-                voff[i] = mn < rows_left ? (uint32_t)(r * sk_bytes + mn * 2) : kOob;
+                if constexpr (GLB) {
+                    // rows_left is a multiple of 8 for an M/N-major 16-bit operand
+                    const int64_t mc = mn < rows_left ? mn : rows_left - 8;
+                    voff[i] = (uint32_t)(r * sk_bytes + mc * 2);
+                } else {
+                    voff[i] = mn < rows_left ? (uint32_t)(r * sk_bytes + mn * 2) : kOob;
+                }
             }
         }
     }
-    // The buffer resource and K bound of one stage's DMA.
+    // The buffer resource (GLB: the 64-bit base in x, y) and K bound of one
+    // stage's DMA.
     struct Stage {
         i32x4_t rsrc;
         int64_t k0;
@@ -1098,6 +1120,17 @@ struct DirectLoader {
     };
     __device__ __forceinline__ Stage prep(uint8_t *dst, int kt) const {
         Stage st;
+        if constexpr (GLB) {
+            const int last = (int)(K / BKS) - 1;  // K >= BKS, a multiple of BKS
+            st.k0 = (int64_t)(kt < last ? kt : last) * BKS;
+            const uint64_t addr = (uint64_t)(base + st.k0 * sk_bytes);
+            st.rsrc.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
+            st.rsrc.y = __builtin_amdgcn_readfirstlane((int)(uint32_t)(addr >> 32));
+            st.rsrc.z = st.rsrc.w = 0;
+            st.k_ok = true;
+            st.lds_base = (uint32_t)(uintptr_t)dst;
+            return st;
+        }
         st.k0 = (int64_t)kt * BKS;
         int64_t nb = nbytes - st.k0 * sk_bytes;
         nb = nb < 0 ? 0 : (nb > (int64_t)kMaxRec ? (int64_t)kMaxRec : nb);
@@ -1115,6 +1148,13 @@ struct DirectLoader {
     __device__ __forceinline__ void issue_one(const Stage &st, int wave) const {
         const int blk = wave + I * kWaves;
         const uint32_t m0 = __builtin_amdgcn_readfirstlane(st.lds_base + blk * 1024);
+        if constexpr (GLB) {
+            const char *gb = (const char *)(((uint64_t)(uint32_t)st.rsrc.y << 32) | (uint32_t)st.rsrc.x);
+            // s_nop 4: the wait states the asm needs after SGPR / M0 writes, as below
+            asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff[I]), "s"(gb), "{m0}"(m0)
+                         : "memory");
+            return;
+        }
         bool ok;
         if constexpr (MN)
             ok = st.k0 + krow[I] < K;
@@ -1255,7 +1295,8 @@ __device__ __forceinline__ TileCoord tile_coord(const GemmArgs &p, int64_t wg) {
 // deferred MFMAs (one or more after each) rather than issued as a burst, so
 // the MFMA pipe keeps running while the DMA is issued (at 8192^3 this
 // measured between even and 4 % faster than a burst, depending on the GPU).
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int NS, int BKS, bool AMN, bool BMN>
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int NS, int BKS, bool AMN, bool BMN,
+          bool GLB = false>
 __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dl(GemmArgs p) {
     constexpr int NT = WAVES_M * WAVES_N * 64;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
@@ -1283,8 +1324,8 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dl(GemmArgs
     // instead measured the same).
     constexpr int DW = NT / 64 < 4 ? NT / 64 : 4;
     const bool dma_wave = wave < DW;
-    using LA = DirectLoader<BM, DW * 64, AMN, BKS>;
-    using LB = DirectLoader<BN, DW * 64, BMN, BKS>;
+    using LA = DirectLoader<BM, DW * 64, AMN, BKS, GLB>;
+    using LB = DirectLoader<BN, DW * 64, BMN, BKS, GLB>;
     LA la((const char *)p.a + (tc.offa + m0 * p.sam) * 2, p.sam, p.sak, p.M - m0, p.K, wave, lane);
     LB lb((const char *)p.b + (tc.offb + n0 * p.sbn) * 2, p.sbn, p.sbk, p.N - n0, p.K, wave, lane);
     constexpr int kLoadsPerStage = LA::kPer + LB::kPer;
@@ -1578,7 +1619,7 @@ struct FragReader16 {
 // spacing 1 / 2 / 3, per-wave DMA offsets; this one measured best).  The
 // second group of each stage is deferred past the barrier.  The MFMA sums
 // equal those of the 32x32x16 kernels bit for bit on the shapes tested.
-template <typename T, int DF = 8, int DS = 4, int RS = 2>
+template <typename T, bool GLB = false, int DF = 8, int DS = 4, int RS = 2>
 __global__ void __launch_bounds__(256) gemm_kernel_dli16(GemmArgs p) {
     constexpr int BM = 256, BN = 256, BKS = 64, NT = 256, WAVES_N = 2;
     constexpr int WM = 128, WN = 128, TM = 8, TN = 8;  // 16x16 blocks per wave
@@ -1593,8 +1634,8 @@ __global__ void __launch_bounds__(256) gemm_kernel_dli16(GemmArgs p) {
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const TileCoord tc = tile_coord<BM, BN>(p, blockIdx.x);
     const int64_t m0 = tc.m0, n0 = tc.n0;
-    using LA = DirectLoader<BM, NT, false, BKS>;
-    using LB = DirectLoader<BN, NT, false, BKS>;
+    using LA = DirectLoader<BM, NT, false, BKS, GLB>;
+    using LB = DirectLoader<BN, NT, false, BKS, GLB>;
     LA la((const char *)p.a + (tc.offa + m0 * p.sam) * 2, p.sam, p.sak, p.M - m0, p.K, wave, lane);
     LB lb((const char *)p.b + (tc.offb + n0 * p.sbn) * 2, p.sbn, p.sbk, p.N - n0, p.K, wave, lane);
     constexpr int L = LA::kPer + LB::kPer;  // DMA instructions per wave per stage

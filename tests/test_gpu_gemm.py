@@ -244,6 +244,49 @@ def test_batched_broadcast_small(hip, dtype):
     assert_close(to_f32(c), O.matmul(a.ora, b.ora), spec_tolerance(dtype, 40), "batched")
 
 
+# ---- the direct-to-LDS DMA through global_load_lds (K a multiple of 64) ------------
+# With K a whole number of 64-k stages the direct-to-LDS kernels issue their
+# DMA as global_load_lds_dwordx4, which has no range check: rows (and
+# M/N-major column chunks) past the operand's edge read the last valid ones
+# and feed only outputs that are never stored.  Ragged M and N on every
+# operand layout, each 16-bit configuration that uses it, must give exactly
+# the buffer-load path's results (OXM_GEMM_GLOBAL_DMA=0), and the oracle's.
+GLOBAL_DMA_SHAPES = [(300, 192, 264), (264, 512, 520), (72, 64, 136), (1000, 1024, 1496)]
+
+
+@pytest.mark.parametrize("cfg", ["1", "2", "7"])
+@pytest.mark.parametrize("la,lb", [("row", "col"), ("row", "row"), ("col", "col"), ("col", "row")])
+def test_global_dma_matches_buffer_dma(hip, monkeypatch, cfg, la, lb):
+    monkeypatch.setenv("OXM_GEMM_CFG", cfg)
+    for si, (m, k, n) in enumerate(GLOBAL_DMA_SHAPES):
+        dtype = BF16 if si % 2 == 0 else F16
+        a = make_operand(dtype, la, m, k, 7000 + si, "a")
+        b = make_operand(dtype, lb, k, n, 8000 + si, "b")
+        log(f"global DMA cfg {cfg} {dtype.name} {la}x{lb} M={m} K={k} N={n}")
+        monkeypatch.setenv("OXM_GEMM_GLOBAL_DMA", "0")
+        c0 = to_f32(hip.matmul(a.dev, b.dev))
+        monkeypatch.setenv("OXM_GEMM_GLOBAL_DMA", "1")
+        c1 = to_f32(hip.matmul(a.dev, b.dev))
+        assert np.array_equal(c0, c1), f"cfg {cfg} {la}x{lb} {m}x{k}x{n}: global and buffer DMA differ"
+        assert_close(c1, O.matmul(a.ora, b.ora), spec_tolerance(dtype, k), f"cfg {cfg} {la}x{lb} {m}x{k}x{n}")
+
+
+def test_global_dma_batched_broadcast(hip, monkeypatch):
+    """Batch offsets and a broadcast B on the global-load DMA path."""
+    rng = np.random.default_rng(9)
+    nb, m, k, n = 3, 200, 128, 136
+    abuf = host_buffer(BF16, rng.uniform(-1, 1, nb * m * k).astype(np.float32))
+    a = Operand(BF16, abuf, (nb, m, k), (m * k, k, 1))
+    bbuf = host_buffer(BF16, rng.uniform(-1, 1, n * k).astype(np.float32))
+    b = Operand(BF16, bbuf, (1, k, n), (n * k, 1, k))
+    outs = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("OXM_GEMM_GLOBAL_DMA", flag)
+        outs.append(to_f32(hip.matmul(a.dev, b.dev)))
+    assert np.array_equal(outs[0], outs[1])
+    assert_close(outs[1], O.matmul(a.ora, b.ora), spec_tolerance(BF16, k), "batched global DMA")
+
+
 @pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "f16"])
 def test_batched_direct_to_lds(hip, dtype):
     """Batched 16-bit GEMM whose operands both qualify for the direct-to-LDS
