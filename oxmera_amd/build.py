@@ -39,14 +39,90 @@ def _hipcc() -> str:
     return exe
 
 
+# Units whose kernels issue global_load_lds with the short hazard pad: their
+# device assembly is kept (-save-temps) and checked by check_dma_hazards.
+CHECKED = ("gemm_bf16.hip", "gemm_f16.hip")
+
+
 def _compile(src: str) -> Path:
     obj = BUILD / (src.replace(".", "_") + ".o")
     lang = ["-x", "hip"]
-    cmd = [_hipcc(), *COMMON, *lang, "-c", str(CSRC / src), "-o", str(obj)]
+    extra = []
+    if src in CHECKED:
+        tmp = BUILD / ("tmp_" + src.replace(".", "_"))
+        tmp.mkdir(exist_ok=True)
+        extra = [f"-save-temps={'obj'}"]
+        obj_in_tmp = tmp / obj.name
+        cmd = [_hipcc(), *COMMON, *extra, *lang, "-c", str(CSRC / src), "-o", str(obj_in_tmp)]
+    else:
+        cmd = [_hipcc(), *COMMON, *lang, "-c", str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    if src in CHECKED:
+        asm = [f for f in tmp.iterdir() if f.name.endswith("gfx950.s")]
+        problems = [p for f in asm for p in check_dma_hazards(f.read_text())]
+        if not asm:
+            problems = [f"no device assembly for {src}"]
+        if problems:
+            raise RuntimeError(f"{src}: DMA hazard check failed:\n" + "\n".join(problems[:20]))
+        os.replace(obj_in_tmp, obj)
+        shutil.rmtree(tmp, ignore_errors=True)
     return obj
+
+
+def _sgprs(tok: str) -> set:
+    """SGPR numbers named by an operand token: s5, s[2:3]."""
+    import re
+    m = re.fullmatch(r"s(\d+)", tok)
+    if m:
+        return {int(m.group(1))}
+    m = re.fullmatch(r"s\[(\d+):(\d+)\]", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    return set()
+
+
+def check_dma_hazards(asm: str) -> list:
+    """Every global_load_lds_dwordx4 preceded by the short pad (s_nop 0) must
+    have no VALU write of its base SGPRs within the 5 wait states a VMEM read
+    of a VALU-written SGPR needs (each instruction counts one, s_nop N counts
+    N + 1; a label ends the search as unsafe, since a predecessor block could
+    end with such a write).  Returns a description of each violation."""
+    import re
+    lines = []
+    for raw in asm.splitlines():
+        t = raw.split(";", 1)[0].strip()
+        if not t or (t.startswith(".") and not t.endswith(":")):
+            continue  # blank or a directive (labels such as .LBB0_3: are kept)
+        lines.append(t)
+    problems = []
+    for i, t in enumerate(lines):
+        if not t.startswith("global_load_lds_dwordx4"):
+            continue
+        ops = [o.strip() for o in t.split(None, 1)[1].split(",")]
+        base = _sgprs(ops[1]) if len(ops) > 1 else set()
+        # the asm block: s_mov_b32 m0, sX / s_nop N / the load
+        if i < 2 or not lines[i - 1].startswith("s_nop") or not lines[i - 2].startswith("s_mov_b32 m0"):
+            problems.append(f"unexpected sequence before: {t}")
+            continue
+        if int(lines[i - 1].split()[1], 0) >= 4:
+            continue  # the full pad
+        waits, j = 0, i - 1
+        while j >= 0 and waits < 5:
+            u = lines[j]
+            if u.endswith(":"):
+                problems.append(f"block boundary within 5 wait states of a short-pad DMA: {t}")
+                break
+            mn = u.split()[0]
+            if mn.startswith("v_"):
+                dst = [o.strip() for o in u.split(None, 1)[1].split(",")][:2] if " " in u else []
+                if any(_sgprs(d) & base for d in dst):
+                    problems.append(f"VALU write of the DMA base within {waits} wait states: {u} -> {t}")
+                    break
+            waits += int(u.split()[1], 0) + 1 if mn == "s_nop" else 1
+            j -= 1
+    return problems
 
 
 CLI_SRC = PKG / "cli" / "doctor.cpp"

@@ -1150,9 +1150,23 @@ struct DirectLoader {
         const uint32_t m0 = __builtin_amdgcn_readfirstlane(st.lds_base + blk * 1024);
         if constexpr (GLB) {
             const char *gb = (const char *)(((uint64_t)(uint32_t)st.rsrc.y << 32) | (uint32_t)st.rsrc.x);
-            // s_nop 4: the wait states the asm needs after SGPR / M0 writes, as below
-            asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff[I]), "s"(gb), "{m0}"(m0)
-                         : "memory");
+            // M0 is written inside the asm by an SALU move, which the DMA may
+            // read after one wait state (s_nop 0).  The base SGPRs come from
+            // prep(), possibly through v_readfirstlane: a VMEM read of an SGPR
+            // a VALU wrote needs 5 wait states, which the first instruction of
+            // each prepared stage (I == 0, issued before the others) supplies
+            // with s_nop 4; the later ones follow it.  The short pad took the
+            // one-wave kernel's stage from 2554 to 2316 cycles.  The build
+            // checks the emitted code for a VALU write of a DMA's base SGPRs
+            // within 5 wait states (oxmera_amd/build.py).
+            if constexpr (I == 0)
+                asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff[I]), "s"(gb),
+                             "s"(m0)
+                             : "memory", "m0");
+            else
+                asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff[I]), "s"(gb),
+                             "s"(m0)
+                             : "memory", "m0");
             return;
         }
         bool ok;
