@@ -704,16 +704,16 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     int ld_a = classify((const char *)g.a, g.sam, g.sak, g.M, K, g.bsa, nbd, es, ts.bm);
     int ld_b = classify((const char *)g.b, g.sbn, g.sbk, N, K, g.bsb, nbd, es, ts.bn);
     // The 16x16x32 one-wave kernel in the band where it measured faster than
-    // the 2x4-wave kernel (interleaved medians, K-major bf16 operands, both
-    // with the global-load DMA): 1024 to 2304 256x256 tiles and K of 8192 to
-    // 12288 (8192^3: 0.767 vs 0.793 ms; 8192^2 x K 12288, 16384 x 8192 x
-    // 8192, 12288^2 x 8192: 1.2-3.6 % faster); outside it (K 4096 or 16384,
-    // 512 or 4096 tiles) and under a GELU / GELU' or column-sum epilogue it
-    // measured 1-20 % slower.
+    // (or level with) the 2x4-wave kernel: interleaved medians, K-major bf16
+    // operands, both with the global-load DMA and its short hazard pad --
+    // K of 4096 to 12288 and at least 512 256x256 tiles (8192^3: 0.742 vs
+    // 0.790 ms; 576 to 4096 tiles at K 4096-12288: 1.1-5.5 % faster, one
+    // 2048-tile K 4096 shape level); at K 16384, on 256 tiles and under a
+    // GELU / GELU' or column-sum epilogue it measured level to 20 % slower.
     if (!forced && cfg == oxm::kCfgH_256 && ld_a == oxm::kLdK && ld_b == oxm::kLdK && ep->act == OXM_ACT_NONE &&
-        !ep->colsum && K >= 8192 && K <= 12288) {
+        !ep->colsum && K >= 4096 && K <= 12288) {
         const int64_t n256 = ((g.M + 255) / 256) * ((N + 255) / 256) * batch;
-        if (n256 >= 1024 && n256 <= 2304) cfg = oxm::kCfgH_256_1W16;
+        if (n256 >= 512) cfg = oxm::kCfgH_256_1W16;
     }
     int64_t ntiles = ((g.M + ts.bm - 1) / ts.bm) * ((N + ts.bn - 1) / ts.bn) * batch;
     if (ntiles > 0x7fffffffLL) return fail(OXM_E_NOT_IMPLEMENTED, "matmul is not implemented for %lld tiles", (long long)ntiles);
