@@ -3,6 +3,7 @@
 // (gemm_f32.hip, gemm_bf16.hip, gemm_f16.hip) so they build in parallel.
 #include <cstdlib>
 
+#include "gemm_dispatch.hpp"
 #include "gemm_launch.hpp"
 #include "gemm_kernels.hpp"
 
@@ -12,10 +13,29 @@ hipError_t launch_gemm_f32(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipSt
 hipError_t launch_gemm_bf16(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipStream_t s);
 hipError_t launch_gemm_f16(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipStream_t s);
 
+static bool env_off(const char *name) {
+    const char *v = getenv(name);
+    return v && v[0] == '0';
+}
+
 bool use_global_dma(const GemmArgs &a) {
-    if (a.K < 64 || a.K % 64 != 0) return false;
-    const char *v = getenv("OXM_GEMM_GLOBAL_DMA");
-    return !(v && v[0] == '0');
+    return a.K >= 64 && a.K % 64 == 0 && !env_off("OXM_GEMM_GLOBAL_DMA");
+}
+
+bool use_global_dma_f32(const GemmArgs &a) {
+    return a.K >= 32 && a.K % 32 == 0 && !env_off("OXM_GEMM_GLOBAL_DMA");
+}
+
+bool use_f32_dma(const GemmArgs &a, int la, int lb) {
+    if (env_off("OXM_GEMM_F32_DMA")) return false;
+    if ((la != kLdK && la != kLdMN) || (lb != kLdK && lb != kLdMN)) return false;
+    // every row (K-major) or k-row (M/N-major) of both operands starts 16-byte aligned
+    if ((uintptr_t)a.a % 16 != 0 || (uintptr_t)a.b % 16 != 0) return false;
+    const int64_t ra = la == kLdK ? a.sam : a.sak, rb = lb == kLdK ? a.sbn : a.sbk;
+    if (ra % 4 != 0 || rb % 4 != 0) return false;
+    for (int d = 0; d < a.nbd; ++d)
+        if (a.bsa[d] % 4 != 0 || a.bsb[d] % 4 != 0) return false;
+    return true;
 }
 
 TileShape tile_shape(int cfg) {

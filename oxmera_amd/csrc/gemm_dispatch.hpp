@@ -19,6 +19,26 @@ hipError_t launch_one(const GemmArgs &a, hipStream_t s) {
 // call, like OXM_GEMM_CFG).
 bool use_global_dma(const GemmArgs &a);
 
+// f32 on 256x256 tiles: the direct-to-LDS kernel (gemm_kernel_dlf32) serves
+// K- or M/N-contiguous operands whose rows all start 16-byte aligned, unless
+// OXM_GEMM_F32_DMA=0 (read at each call) keeps the register-staged kernel;
+// its DMA goes through global_load_lds when K is a multiple of 32 and
+// OXM_GEMM_GLOBAL_DMA is not 0.
+bool use_f32_dma(const GemmArgs &a, int la, int lb);
+bool use_global_dma_f32(const GemmArgs &a);
+
+template <bool AMN, bool BMN>
+hipError_t launch_dlf32(GemmArgs a, hipStream_t s) {
+    a.group_m = 4;
+    int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n * a.batch;
+    dim3 grid((unsigned)ntiles), block(512);
+    if (use_global_dma_f32(a))
+        hipLaunchKernelGGL((gemm_kernel_dlf32<AMN, BMN, true>), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((gemm_kernel_dlf32<AMN, BMN, false>), grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
 // Direct-to-LDS kernel (16-bit operands, each K- or M/N-contiguous).
 template <typename T, int BM, int BN, int WM, int WN, int NS, int BKS, bool AMN, bool BMN, bool GLB = false>
 hipError_t launch_dl(GemmArgs a, hipStream_t s) {

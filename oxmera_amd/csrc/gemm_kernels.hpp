@@ -1749,4 +1749,239 @@ __global__ void __launch_bounds__(256) gemm_kernel_dli16(GemmArgs p) {
                                                  n0 + wn * WN);
 }
 
+// ---- f32 direct-to-LDS (256x256 tiles) -----------------------------------------
+//
+// The register-staged f32 kernel moves every operand byte through VGPRs
+// (global loads, a 4x4 transpose for an M/N-major operand, ds_write_b128).
+// Here both operands go global -> LDS by DMA, as in the 16-bit kernels:
+// 4096^3 row-major x row-major 0.987 -> 0.924 ms (88.5 -> 94.6 % of the f32
+// MFMA peak), bit-identical.  A 32-k stage of a 256-row operand is 32 KB in
+// either orientation.
+
+// K-major f32 operand: a 32-k row is 128 bytes, the same bytes as a 64-k row
+// of a 16-bit operand, so DirectLoader / FragReader serve it unchanged with
+// strides and K counted in 16-bit units.  The fragments then hold 4 f32 k
+// values per lane, k = 8 g + 4 (lane / 32) + s, as Mma<float> takes them.
+template <bool GLB>
+struct F32LoaderK : DirectLoader<256, 256, false, 64, GLB> {
+    using Base = DirectLoader<256, 256, false, 64, GLB>;
+    __device__ __forceinline__ F32LoaderK(const char *b, int64_t s_mn, int64_t rows_left, int64_t k, int wave,
+                                          int lane)
+        : Base(b, 2 * s_mn, 1, rows_left, 2 * k, wave, lane) {}
+};
+
+// M/N-major f32 operand (256 values along M or N contiguous per k): one 1 KB
+// DMA block per k-row; the k-rows whose bit 2 is set are stored rotated by
+// 128 bytes, so a fragment read (lanes 0-31 at k-row k, lanes 32-63 at
+// k + 4, 32 consecutive values each) touches 64 distinct banks.  Lane L of
+// block b fetches the 16 bytes of column chunk (L - rot(b)) mod 64.  Past the
+// operand's M/N edge: kOob (buffer form, reads zeros) or the last valid chunk
+// (GLB: those columns feed only outputs that are never stored); past K: kOob,
+// or (GLB, K a multiple of 32) the last step again into a stage nobody reads.
+template <bool GLB>
+struct F32LoaderMN {
+    static constexpr int kWaves = 4;
+    static constexpr int kPer = 32 / kWaves;  // DMA instructions per wave per stage
+    const char *base;
+    int64_t K, sk_bytes, nbytes, cols_left;
+    int lane;
+    struct Stage {
+        i32x4_t rsrc;
+        int64_t k0;
+        uint32_t lds_base;
+    };
+    __device__ __forceinline__ F32LoaderMN(const char *b, int64_t s_k, int64_t cols, int64_t k, int /*wave*/,
+                                           int ln)
+        : base(b), K(k), sk_bytes(s_k * 4), cols_left(cols), lane(ln) {
+        const int64_t cols_here = cols < 256 ? cols : 256;
+        nbytes = (k - 1) * sk_bytes + cols_here * 4;
+    }
+    __device__ __forceinline__ Stage prep(uint8_t *dst, int kt) const {
+        Stage st;
+        if constexpr (GLB) {
+            const int last = (int)(K / 32) - 1;  // K >= 32, a multiple of 32
+            st.k0 = (int64_t)(kt < last ? kt : last) * 32;
+            const uint64_t addr = (uint64_t)(base + st.k0 * sk_bytes);
+            st.rsrc.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
+            st.rsrc.y = __builtin_amdgcn_readfirstlane((int)(uint32_t)(addr >> 32));
+            st.rsrc.z = st.rsrc.w = 0;
+        } else {
+            st.k0 = (int64_t)kt * 32;
+            int64_t nb = nbytes - st.k0 * sk_bytes;
+            nb = nb < 0 ? 0 : (nb > (int64_t)kMaxRec ? (int64_t)kMaxRec : nb);
+            const uint64_t addr = (uint64_t)(base + st.k0 * sk_bytes);
+            st.rsrc.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
+            st.rsrc.y = __builtin_amdgcn_readfirstlane((int)(uint32_t)(addr >> 32) & 0xffff);
+            st.rsrc.z = __builtin_amdgcn_readfirstlane((int)nb);
+            st.rsrc.w = 0x00020000;
+        }
+        st.lds_base = (uint32_t)(uintptr_t)dst;
+        return st;
+    }
+    template <int I>
+    __device__ __forceinline__ void issue_one(const Stage &st, int wave) const {
+        const int blk = wave + I * kWaves;
+        const uint32_t m0 = __builtin_amdgcn_readfirstlane(st.lds_base + blk * 1024);
+        const int c = (lane - ((blk >> 2) & 1) * 8) & 63;
+        int64_t col = 4 * c;
+        if constexpr (GLB) {
+            if (col >= cols_left) col = cols_left - 4;  // cols_left is a multiple of 4
+            const uint32_t vo = (uint32_t)(blk * sk_bytes + col * 4);
+            const char *gb = (const char *)(((uint64_t)(uint32_t)st.rsrc.y << 32) | (uint32_t)st.rsrc.x);
+            // pads as in DirectLoader: the first DMA of a prepared stage waits
+            // out a VALU write of the base SGPRs, the later ones only M0's
+            if constexpr (I == 0)
+                asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(vo), "s"(gb),
+                             "s"(m0)
+                             : "memory", "m0");
+            else
+                asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(vo), "s"(gb),
+                             "s"(m0)
+                             : "memory", "m0");
+        } else {
+            const uint32_t vo =
+                (col < cols_left && st.k0 + blk < K) ? (uint32_t)(blk * sk_bytes + col * 4) : kOob;
+            asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(vo), "s"(st.rsrc), "{m0}"(m0)
+                         : "memory");
+        }
+    }
+    __device__ __forceinline__ void issue(uint8_t *dst, int kt, int wave) {
+        const Stage st = prep(dst, kt);
+        static_for<0, kPer>([&](auto ic) { issue_one<decltype(ic)::value>(st, wave); });
+    }
+};
+
+// Fragments of an M/N-major f32 operand from the rotated stage: TILES tiles
+// of 32 values starting at mn0; lane l supplies mn0 + 32 I + l % 32 at
+// k = 8 g + 4 (l / 32) + s (s = 0..3), four ds_read_b32 per fragment.
+template <int TILES>
+struct F32FragMN {
+    uint32_t region;
+    int mn0, lane;
+    __device__ __forceinline__ F32FragMN(uint32_t r, int m, int l) : region(r), mn0(m), lane(l) {}
+    __device__ __forceinline__ void read(const uint8_t *stage, int g, uint4 (&out)[TILES]) const {
+#pragma unroll
+        for (int i = 0; i < TILES; ++i) {
+            const int c = mn0 + 32 * i + (lane & 31);
+            uint32_t v[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int k = 8 * g + 4 * (lane >> 5) + s;
+                v[s] = *(const uint32_t *)(stage + region + k * 1024 + ((c * 4 + ((k >> 2) & 1) * 128) & 1023));
+            }
+            out[i] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+    }
+};
+
+// 256x256 tile, 2x4 waves of 128x64, 32-k stages (two in flight), the DMA
+// issued by waves 0-3; the same pipeline as gemm_kernel_dl.
+template <bool AMN, bool BMN, bool GLB>
+__global__ void __launch_bounds__(512) gemm_kernel_dlf32(GemmArgs p) {
+    constexpr int BM = 256, BN = 256, WAVES_N = 4, NT = 512, NS = 2;
+    constexpr int WM = 128, WN = 64, TM = 4, TN = 2, kG = 4;
+    constexpr int kStageA = 32768, kStageB = 32768, kStage = kStageA + kStageB;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const TileCoord tc = tile_coord<BM, BN>(p, blockIdx.x);
+    const int64_t m0 = tc.m0, n0 = tc.n0;
+    const bool dma_wave = wave < 4;
+    using LA = typename std::conditional<AMN, F32LoaderMN<GLB>, F32LoaderK<GLB>>::type;
+    using LB = typename std::conditional<BMN, F32LoaderMN<GLB>, F32LoaderK<GLB>>::type;
+    LA la((const char *)p.a + (tc.offa + m0 * p.sam) * 4, AMN ? p.sak : p.sam, p.M - m0, p.K, wave, lane);
+    LB lb((const char *)p.b + (tc.offb + n0 * p.sbn) * 4, BMN ? p.sbk : p.sbn, p.N - n0, p.K, wave, lane);
+    constexpr int kLoadsPerStage = LA::kPer + LB::kPer;
+    using FA = typename std::conditional<AMN, F32FragMN<TM>, FragReader<BM, TM, false, 64>>::type;
+    using FB = typename std::conditional<BMN, F32FragMN<TN>, FragReader<BN, TN, false, 64>>::type;
+    const FA fra(0, wm * WM, lane);
+    const FB frb(kStageA, wn * WN, lane);
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x16_t{};
+    uint4 fa[2][TM], fb[2][TN];
+
+    const int nk = (int)((p.K + 31) / 32);
+    // prologue: stage 0, then (after it landed) stage 1 in flight
+    if (dma_wave) {
+        la.issue(lds, 0, wave);
+        lb.issue(lds + kStageA, 0, wave);
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (dma_wave) {
+        la.issue(lds + kStage, 1, wave);
+        lb.issue(lds + kStage + kStageA, 1, wave);
+    }
+    fra.read(lds, 0, fa[0]);
+    frb.read(lds, 0, fb[0]);
+    constexpr int kQ = TM * TN * 4;  // MFMAs per fragment group (Mma<float> issues four)
+    constexpr int kReads = TM * (AMN ? 4 : 1) + TN * (BMN ? 4 : 1);
+    constexpr int kPerR = (kReads + kQ / 2 - 1) / (kQ / 2);
+    int cur = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+        uint8_t *stage = lds + cur * kStage;
+        const typename LA::Stage sta = la.prep(stage, kt + NS);
+        const typename LB::Stage stb = lb.prep(stage + kStageA, kt + NS);
+        static_for<0, kG - 1>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            fra.read(stage, g + 1, fa[(g + 1) & 1]);
+            frb.read(stage, g + 1, fb[(g + 1) & 1]);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) Mma<float>::run(acc[i][j], fa[g & 1][i], fb[g & 1][j]);
+            // group g+1's fragment reads over the first half of group g's MFMAs
+            static_for<0, kQ>([&](auto qc) {
+                constexpr int q = decltype(qc)::value;
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                constexpr int left = kReads - q * kPerR;
+                constexpr int nr = q < kQ / 2 ? (left < kPerR ? (left > 0 ? left : 0) : kPerR) : 0;
+                if constexpr (nr > 0) __builtin_amdgcn_sched_group_barrier(0x100, nr, 0);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        // every LDS read of step kt landed; this wave's DMA of step kt+1 landed
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & ~(0xF << 8));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        constexpr int gl = (kG - 1) & 1;
+        cur ^= 1;
+        const uint8_t *next = lds + cur * kStage;
+        fra.read(next, 0, fa[0]);
+        frb.read(next, 0, fb[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        // the deferred group's MFMAs, the DMA of step kt+2 (into the stage
+        // just consumed) spread over them
+        constexpr int Q = TM * TN, L = kLoadsPerStage;
+        static_for<0, Q>([&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            Mma<float>::run(acc[q / TN][q % TN], fa[gl][q / TN], fb[gl][q % TN]);
+            if (dma_wave) {
+                static_for<q * L / Q, (q + 1) * L / Q>([&](auto lc) {
+                    constexpr int l = decltype(lc)::value;
+                    if constexpr (l < LA::kPer)
+                        la.template issue_one<l>(sta, wave);
+                    else
+                        lb.template issue_one<l - LA::kPer>(stb, wave);
+                });
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __syncthreads();
+    epilogue_lds<NT, WM, WN, TM, TN, NS * kStage>(p, acc, lds, wave, lane, tc.bidx * p.M * p.N, m0 + wm * WM,
+                                                  n0 + wn * WN);
+}
+
 }  // namespace oxm
+

@@ -164,6 +164,53 @@ def test_tile_configs_f32(hip, monkeypatch, cfg, la, lb):
                      f"f32 cfg {cfg} {la}x{lb} {m}x{k}x{n}")
 
 
+# ---- the f32 direct-to-LDS kernel (256x256 tiles) ------------------------------------
+# For 256x256 f32 tiles of K- or M/N-contiguous, 16-byte aligned operands the
+# dispatcher takes the direct-to-LDS kernel (OXM_GEMM_F32_DMA=0 keeps the
+# register-staged one), its DMA through global_load_lds when K is a multiple
+# of 32 (OXM_GEMM_GLOBAL_DMA=0: the buffer form).  On ragged M/N, K a
+# multiple of 32 or not, every K/MN layout pair: the three paths give the
+# same numbers, and the oracle's.
+F32_DMA_SHAPES = [(300, 256, 264), (264, 200, 520), (1000, 1024, 1000), (64, 96, 68)]
+
+
+@pytest.mark.parametrize("la,lb", [("row", "row"), ("row", "col"), ("col", "row"), ("col", "col")])
+def test_f32_dma_kernel_matches_register_kernel(hip, monkeypatch, la, lb):
+    monkeypatch.setenv("OXM_GEMM_CFG_F32", "5")
+    for si, (m, k, n) in enumerate(F32_DMA_SHAPES):
+        a = make_operand(F32, la, m, k, 9000 + si, "a")
+        b = make_operand(F32, lb, k, n, 9100 + si, "b")
+        log(f"f32 DMA {la}x{lb} M={m} K={k} N={n}")
+        outs = {}
+        for dma, glb in (("0", "1"), ("1", "0"), ("1", "1")):
+            monkeypatch.setenv("OXM_GEMM_F32_DMA", dma)
+            monkeypatch.setenv("OXM_GEMM_GLOBAL_DMA", glb)
+            outs[(dma, glb)] = to_f32(hip.matmul(a.dev, b.dev))
+        ref = outs[("0", "1")]
+        for key, c in outs.items():
+            assert np.array_equal(c, ref), f"{la}x{lb} {m}x{k}x{n}: path {key} differs from the register kernel"
+        assert_close(ref, O.matmul(a.ora, b.ora), spec_tolerance(F32, k), f"f32 DMA {la}x{lb} {m}x{k}x{n}")
+
+
+def test_f32_dma_kernel_epilogue(hip, monkeypatch):
+    """Bias + GELU with the pre-activation saved, on the f32 direct-to-LDS
+    kernel (K a multiple of 32: the global-load DMA)."""
+    monkeypatch.setenv("OXM_GEMM_CFG_F32", "5")
+    rng = np.random.default_rng(31)
+    m, k, n = 300, 256, 264
+    a = contiguous_operand(F32, rng.normal(0, 1, (m, k)))
+    b = make_operand(F32, "row", k, n, 32, "b")
+    bias_vals = rng.normal(0, 0.5, n).astype(np.float32)
+    bias = ox.Tensor.from_numpy(bias_vals, ox.Device.rocm(0), F32)
+    z = ox.Tensor.empty((m, n), F32, ox.Device.rocm(0))
+    c = hip.matmul(a.dev, b.dev, bias=bias, act=ox.ACT_GELU, aux=z)
+    ref, ref_z = O.matmul(a.ora, b.ora, out_dtype=O.F32, bias=bias_vals, bias_dtype=O.F32, act=O.ACT_GELU,
+                          want_aux=True)
+    tol = spec_tolerance(F32, k)
+    assert_close(to_f32(z), ref_z, tol, "pre-activation")
+    assert_close(to_f32(c), ref, tol, "gelu output")
+
+
 # ---- row strip: the leftover rows of a 256x256-tiled GEMM ----------------------------
 # M = 2048 + r with N = 8192: 8 tile-rows x 32 tile-columns fill the 256 CUs
 # once, so r <= 16 leftover rows run on the strip kernel instead of a second,
