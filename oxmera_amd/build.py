@@ -41,7 +41,7 @@ def _hipcc() -> str:
 
 # Units whose kernels issue global_load_lds with the short hazard pad: their
 # device assembly is kept (-save-temps) and checked by check_dma_hazards.
-CHECKED = ("gemm_bf16.hip", "gemm_f16.hip")
+CHECKED = ("gemm_bf16.hip", "gemm_f16.hip", "gemm_f32.hip")
 
 
 def _compile(src: str) -> Path:
