@@ -1762,26 +1762,30 @@ __global__ void __launch_bounds__(256) gemm_kernel_dli16(GemmArgs p) {
 // of a 16-bit operand, so DirectLoader / FragReader serve it unchanged with
 // strides and K counted in 16-bit units.  The fragments then hold 4 f32 k
 // values per lane, k = 8 g + 4 (lane / 32) + s, as Mma<float> takes them.
-template <bool GLB>
-struct F32LoaderK : DirectLoader<256, 256, false, 64, GLB> {
-    using Base = DirectLoader<256, 256, false, 64, GLB>;
+template <int ROWS, bool GLB>
+struct F32LoaderK : DirectLoader<ROWS, 256, false, 64, GLB> {
+    using Base = DirectLoader<ROWS, 256, false, 64, GLB>;
     __device__ __forceinline__ F32LoaderK(const char *b, int64_t s_mn, int64_t rows_left, int64_t k, int wave,
                                           int lane)
         : Base(b, 2 * s_mn, 1, rows_left, 2 * k, wave, lane) {}
 };
 
-// M/N-major f32 operand (256 values along M or N contiguous per k): one 1 KB
-// DMA block per k-row; the k-rows whose bit 2 is set are stored rotated by
+// M/N-major f32 operand (ROWS = 256 or 128 values along M or N contiguous
+// per k): a k-row of the tile is ROWS * 4 bytes, a 1 KB DMA block holds
+// 256 / ROWS of them; the k-rows whose bit 2 is set are stored rotated by
 // 128 bytes, so a fragment read (lanes 0-31 at k-row k, lanes 32-63 at
 // k + 4, 32 consecutive values each) touches 64 distinct banks.  Lane L of
-// block b fetches the 16 bytes of column chunk (L - rot(b)) mod 64.  Past the
-// operand's M/N edge: kOob (buffer form, reads zeros) or the last valid chunk
-// (GLB: those columns feed only outputs that are never stored); past K: kOob,
-// or (GLB, K a multiple of 32) the last step again into a stage nobody reads.
-template <bool GLB>
+// block b fills k-row 256 b / ROWS + L / (ROWS / 4) with the 16 bytes of
+// column chunk (L mod ROWS / 4 - rot) mod ROWS / 4.  Past the operand's M/N
+// edge: kOob (buffer form, reads zeros) or the last valid chunk (GLB: those
+// columns feed only outputs that are never stored); past K: kOob, or (GLB,
+// K a multiple of 32) the last step again into a stage nobody reads.
+template <int ROWS, bool GLB>
 struct F32LoaderMN {
+    static_assert(ROWS == 256 || ROWS == 128, "256- or 128-wide tiles");
     static constexpr int kWaves = 4;
-    static constexpr int kPer = 32 / kWaves;  // DMA instructions per wave per stage
+    static constexpr int kRowBytes = ROWS * 4, kRowsPerBlock = 1024 / kRowBytes, kLanesPerRow = ROWS / 4;
+    static constexpr int kPer = 32 / kRowsPerBlock / kWaves;  // DMA instructions per wave per stage
     const char *base;
     int64_t K, sk_bytes, nbytes, cols_left;
     int lane;
@@ -1793,7 +1797,7 @@ struct F32LoaderMN {
     __device__ __forceinline__ F32LoaderMN(const char *b, int64_t s_k, int64_t cols, int64_t k, int /*wave*/,
                                            int ln)
         : base(b), K(k), sk_bytes(s_k * 4), cols_left(cols), lane(ln) {
-        const int64_t cols_here = cols < 256 ? cols : 256;
+        const int64_t cols_here = cols < ROWS ? cols : ROWS;
         nbytes = (k - 1) * sk_bytes + cols_here * 4;
     }
     __device__ __forceinline__ Stage prep(uint8_t *dst, int kt) const {
@@ -1822,11 +1826,12 @@ struct F32LoaderMN {
     __device__ __forceinline__ void issue_one(const Stage &st, int wave) const {
         const int blk = wave + I * kWaves;
         const uint32_t m0 = __builtin_amdgcn_readfirstlane(st.lds_base + blk * 1024);
-        const int c = (lane - ((blk >> 2) & 1) * 8) & 63;
+        const int kr = blk * kRowsPerBlock + lane / kLanesPerRow;
+        const int c = ((lane % kLanesPerRow) - ((kr >> 2) & 1) * 8) & (kLanesPerRow - 1);
         int64_t col = 4 * c;
         if constexpr (GLB) {
             if (col >= cols_left) col = cols_left - 4;  // cols_left is a multiple of 4
-            const uint32_t vo = (uint32_t)(blk * sk_bytes + col * 4);
+            const uint32_t vo = (uint32_t)(kr * sk_bytes + col * 4);
             const char *gb = (const char *)(((uint64_t)(uint32_t)st.rsrc.y << 32) | (uint32_t)st.rsrc.x);
             // pads as in DirectLoader: the first DMA of a prepared stage waits
             // out a VALU write of the base SGPRs, the later ones only M0's
@@ -1840,7 +1845,7 @@ struct F32LoaderMN {
                              : "memory", "m0");
         } else {
             const uint32_t vo =
-                (col < cols_left && st.k0 + blk < K) ? (uint32_t)(blk * sk_bytes + col * 4) : kOob;
+                (col < cols_left && st.k0 + kr < K) ? (uint32_t)(kr * sk_bytes + col * 4) : kOob;
             asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(vo), "s"(st.rsrc), "{m0}"(m0)
                          : "memory");
         }
@@ -1854,8 +1859,9 @@ struct F32LoaderMN {
 // Fragments of an M/N-major f32 operand from the rotated stage: TILES tiles
 // of 32 values starting at mn0; lane l supplies mn0 + 32 I + l % 32 at
 // k = 8 g + 4 (l / 32) + s (s = 0..3), four ds_read_b32 per fragment.
-template <int TILES>
+template <int TILES, int ROWS>
 struct F32FragMN {
+    static constexpr int kRowBytes = ROWS * 4;
     uint32_t region;
     int mn0, lane;
     __device__ __forceinline__ F32FragMN(uint32_t r, int m, int l) : region(r), mn0(m), lane(l) {}
@@ -1867,20 +1873,23 @@ struct F32FragMN {
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const int k = 8 * g + 4 * (lane >> 5) + s;
-                v[s] = *(const uint32_t *)(stage + region + k * 1024 + ((c * 4 + ((k >> 2) & 1) * 128) & 1023));
+                v[s] = *(const uint32_t *)(stage + region + k * kRowBytes +
+                                           ((c * 4 + ((k >> 2) & 1) * 128) & (kRowBytes - 1)));
             }
             out[i] = make_uint4(v[0], v[1], v[2], v[3]);
         }
     }
 };
 
-// 256x256 tile, 2x4 waves of 128x64, 32-k stages (two in flight), the DMA
-// issued by waves 0-3; the same pipeline as gemm_kernel_dl.
-template <bool AMN, bool BMN, bool GLB>
-__global__ void __launch_bounds__(512) gemm_kernel_dlf32(GemmArgs p) {
-    constexpr int BM = 256, BN = 256, WAVES_N = 4, NT = 512, NS = 2;
-    constexpr int WM = 128, WN = 64, TM = 4, TN = 2, kG = 4;
-    constexpr int kStageA = 32768, kStageB = 32768, kStage = kStageA + kStageB;
+// BM x BN tile (256x256 with 2x4 waves of 128x64, or 128x128 with 2x2 waves
+// of 64x64, two blocks per CU), 32-k stages (two in flight), the DMA issued
+// by waves 0-3; the same pipeline as gemm_kernel_dl.
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool AMN, bool BMN, bool GLB>
+__global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dlf32(GemmArgs p) {
+    constexpr int NT = WAVES_M * WAVES_N * 64, NS = 2;
+    constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, TM = WM / 32, TN = WN / 32, kG = 4;
+    constexpr int kStageA = BM * 128, kStageB = BN * 128, kStage = kStageA + kStageB;
+    static_assert(NT / 64 >= 4, "four DMA waves");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1889,13 +1898,13 @@ __global__ void __launch_bounds__(512) gemm_kernel_dlf32(GemmArgs p) {
     const TileCoord tc = tile_coord<BM, BN>(p, blockIdx.x);
     const int64_t m0 = tc.m0, n0 = tc.n0;
     const bool dma_wave = wave < 4;
-    using LA = typename std::conditional<AMN, F32LoaderMN<GLB>, F32LoaderK<GLB>>::type;
-    using LB = typename std::conditional<BMN, F32LoaderMN<GLB>, F32LoaderK<GLB>>::type;
+    using LA = typename std::conditional<AMN, F32LoaderMN<BM, GLB>, F32LoaderK<BM, GLB>>::type;
+    using LB = typename std::conditional<BMN, F32LoaderMN<BN, GLB>, F32LoaderK<BN, GLB>>::type;
     LA la((const char *)p.a + (tc.offa + m0 * p.sam) * 4, AMN ? p.sak : p.sam, p.M - m0, p.K, wave, lane);
     LB lb((const char *)p.b + (tc.offb + n0 * p.sbn) * 4, BMN ? p.sbk : p.sbn, p.N - n0, p.K, wave, lane);
     constexpr int kLoadsPerStage = LA::kPer + LB::kPer;
-    using FA = typename std::conditional<AMN, F32FragMN<TM>, FragReader<BM, TM, false, 64>>::type;
-    using FB = typename std::conditional<BMN, F32FragMN<TN>, FragReader<BN, TN, false, 64>>::type;
+    using FA = typename std::conditional<AMN, F32FragMN<TM, BM>, FragReader<BM, TM, false, 64>>::type;
+    using FB = typename std::conditional<BMN, F32FragMN<TN, BN>, FragReader<BN, TN, false, 64>>::type;
     const FA fra(0, wm * WM, lane);
     const FB frb(kStageA, wn * WN, lane);
 

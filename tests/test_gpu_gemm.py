@@ -174,13 +174,15 @@ def test_tile_configs_f32(hip, monkeypatch, cfg, la, lb):
 F32_DMA_SHAPES = [(300, 256, 264), (264, 200, 520), (1000, 1024, 1000), (64, 96, 68)]
 
 
+# OXM_GEMM_CFG_F32: 5 = 256x256 tiles, 0 = 128x128 tiles
+@pytest.mark.parametrize("cfg", ["5", "0"])
 @pytest.mark.parametrize("la,lb", [("row", "row"), ("row", "col"), ("col", "row"), ("col", "col")])
-def test_f32_dma_kernel_matches_register_kernel(hip, monkeypatch, la, lb):
-    monkeypatch.setenv("OXM_GEMM_CFG_F32", "5")
+def test_f32_dma_kernel_matches_register_kernel(hip, monkeypatch, la, lb, cfg):
+    monkeypatch.setenv("OXM_GEMM_CFG_F32", cfg)
     for si, (m, k, n) in enumerate(F32_DMA_SHAPES):
         a = make_operand(F32, la, m, k, 9000 + si, "a")
         b = make_operand(F32, lb, k, n, 9100 + si, "b")
-        log(f"f32 DMA {la}x{lb} M={m} K={k} N={n}")
+        log(f"f32 DMA cfg {cfg} {la}x{lb} M={m} K={k} N={n}")
         outs = {}
         for dma, glb in (("0", "1"), ("1", "0"), ("1", "1")):
             monkeypatch.setenv("OXM_GEMM_F32_DMA", dma)
@@ -192,10 +194,11 @@ def test_f32_dma_kernel_matches_register_kernel(hip, monkeypatch, la, lb):
         assert_close(ref, O.matmul(a.ora, b.ora), spec_tolerance(F32, k), f"f32 DMA {la}x{lb} {m}x{k}x{n}")
 
 
-def test_f32_dma_kernel_epilogue(hip, monkeypatch):
+@pytest.mark.parametrize("cfg", ["5", "0"])
+def test_f32_dma_kernel_epilogue(hip, monkeypatch, cfg):
     """Bias + GELU with the pre-activation saved, on the f32 direct-to-LDS
     kernel (K a multiple of 32: the global-load DMA)."""
-    monkeypatch.setenv("OXM_GEMM_CFG_F32", "5")
+    monkeypatch.setenv("OXM_GEMM_CFG_F32", cfg)
     rng = np.random.default_rng(31)
     m, k, n = 300, 256, 264
     a = contiguous_operand(F32, rng.normal(0, 1, (m, k)))
