@@ -48,6 +48,7 @@ TileShape tile_shape(int cfg) {
     case kCfgF32_256: return {256, 256};
     case kCfgH_128: return {128, 128};
     case kCfgF32_64: return {64, 64};
+    case kCfgF32_256x192: return {256, 192};
     default: return {128, 128};
     }
 }

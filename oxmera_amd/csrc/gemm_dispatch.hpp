@@ -19,12 +19,8 @@ hipError_t launch_one(const GemmArgs &a, hipStream_t s) {
 // call, like OXM_GEMM_CFG).
 bool use_global_dma(const GemmArgs &a);
 
-// f32 on 256x256 tiles: the direct-to-LDS kernel (gemm_kernel_dlf32) serves
-// K- or M/N-contiguous operands whose rows all start 16-byte aligned, unless
-// OXM_GEMM_F32_DMA=0 (read at each call) keeps the register-staged kernel;
-// its DMA goes through global_load_lds when K is a multiple of 32 and
-// OXM_GEMM_GLOBAL_DMA is not 0.
-bool use_f32_dma(const GemmArgs &a, int la, int lb);
+// The f32 direct-to-LDS kernel's DMA goes through global_load_lds when K is
+// a multiple of 32 and OXM_GEMM_GLOBAL_DMA is not 0 (use_f32_dma: gemm_launch.hpp).
 bool use_global_dma_f32(const GemmArgs &a);
 
 template <int BM, int BN, int WM, int WN, bool AMN, bool BMN>

@@ -1765,26 +1765,32 @@ __global__ void __launch_bounds__(256) gemm_kernel_dli16(GemmArgs p) {
 template <int ROWS, bool GLB>
 struct F32LoaderK : DirectLoader<ROWS, 256, false, 64, GLB> {
     using Base = DirectLoader<ROWS, 256, false, 64, GLB>;
+    static constexpr int kStageBytes = ROWS * 128;
     __device__ __forceinline__ F32LoaderK(const char *b, int64_t s_mn, int64_t rows_left, int64_t k, int wave,
                                           int lane)
         : Base(b, 2 * s_mn, 1, rows_left, 2 * k, wave, lane) {}
 };
 
-// M/N-major f32 operand (ROWS = 256 or 128 values along M or N contiguous
-// per k): a k-row of the tile is ROWS * 4 bytes, a 1 KB DMA block holds
-// 256 / ROWS of them; the k-rows whose bit 2 is set are stored rotated by
-// 128 bytes, so a fragment read (lanes 0-31 at k-row k, lanes 32-63 at
-// k + 4, 32 consecutive values each) touches 64 distinct banks.  Lane L of
-// block b fills k-row 256 b / ROWS + L / (ROWS / 4) with the 16 bytes of
-// column chunk (L mod ROWS / 4 - rot) mod ROWS / 4.  Past the operand's M/N
-// edge: kOob (buffer form, reads zeros) or the last valid chunk (GLB: those
-// columns feed only outputs that are never stored); past K: kOob, or (GLB,
-// K a multiple of 32) the last step again into a stage nobody reads.
+// M/N-major f32 operand (ROWS = 256, 192 or 128 values along M or N
+// contiguous per k): a k-row of the tile takes 512 bytes of the stage
+// (ROWS = 128) or 1 KB (192 of them used for ROWS = 192), a 1 KB DMA block
+// holds 1024 / kRowBytes of them; the k-rows whose bit 2 is set are stored
+// rotated by 128 bytes, so a fragment read (lanes 0-31 at k-row k, lanes
+// 32-63 at k + 4, 32 consecutive values each) touches 64 distinct banks.
+// Lane L of block b fills k-row b * kRowsPerBlock + L / kLanesPerRow with
+// the 16 bytes of column chunk (L mod kLanesPerRow - rot) mod kLanesPerRow
+// (ROWS = 192: the chunks from 48 on are not used).  Chunks past the tile's
+// or the operand's M/N edge: kOob (buffer form, reads zeros) or the last
+// valid chunk (GLB: those columns feed only outputs that are never stored,
+// or no output); past K: kOob, or (GLB, K a multiple of 32) the last step
+// again into a stage nobody reads.
 template <int ROWS, bool GLB>
 struct F32LoaderMN {
-    static_assert(ROWS == 256 || ROWS == 128, "256- or 128-wide tiles");
+    static_assert(ROWS == 256 || ROWS == 192 || ROWS == 128, "256-, 192- or 128-wide tiles");
     static constexpr int kWaves = 4;
-    static constexpr int kRowBytes = ROWS * 4, kRowsPerBlock = 1024 / kRowBytes, kLanesPerRow = ROWS / 4;
+    static constexpr int kRowBytes = ROWS == 128 ? 512 : 1024, kRowsPerBlock = 1024 / kRowBytes,
+                         kLanesPerRow = kRowBytes / 16;
+    static constexpr int kStageBytes = 32 * kRowBytes;
     static constexpr int kPer = 32 / kRowsPerBlock / kWaves;  // DMA instructions per wave per stage
     const char *base;
     int64_t K, sk_bytes, nbytes, cols_left;
@@ -1829,8 +1835,10 @@ struct F32LoaderMN {
         const int kr = blk * kRowsPerBlock + lane / kLanesPerRow;
         const int c = ((lane % kLanesPerRow) - ((kr >> 2) & 1) * 8) & (kLanesPerRow - 1);
         int64_t col = 4 * c;
+        // the columns this tile reads: a multiple of 4 (M/N a multiple of 4)
+        const int64_t lim = cols_left < ROWS ? cols_left : ROWS;
         if constexpr (GLB) {
-            if (col >= cols_left) col = cols_left - 4;  // cols_left is a multiple of 4
+            if (col >= lim) col = lim - 4;
             const uint32_t vo = (uint32_t)(kr * sk_bytes + col * 4);
             const char *gb = (const char *)(((uint64_t)(uint32_t)st.rsrc.y << 32) | (uint32_t)st.rsrc.x);
             // pads as in DirectLoader: the first DMA of a prepared stage waits
@@ -1845,7 +1853,7 @@ struct F32LoaderMN {
                              : "memory", "m0");
         } else {
             const uint32_t vo =
-                (col < cols_left && st.k0 + kr < K) ? (uint32_t)(kr * sk_bytes + col * 4) : kOob;
+                (col < lim && st.k0 + kr < K) ? (uint32_t)(kr * sk_bytes + col * 4) : kOob;
             asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(vo), "s"(st.rsrc), "{m0}"(m0)
                          : "memory");
         }
@@ -1861,7 +1869,7 @@ struct F32LoaderMN {
 // k = 8 g + 4 (l / 32) + s (s = 0..3), four ds_read_b32 per fragment.
 template <int TILES, int ROWS>
 struct F32FragMN {
-    static constexpr int kRowBytes = ROWS * 4;
+    static constexpr int kRowBytes = ROWS == 128 ? 512 : 1024;
     uint32_t region;
     int mn0, lane;
     __device__ __forceinline__ F32FragMN(uint32_t r, int m, int l) : region(r), mn0(m), lane(l) {}
@@ -1881,16 +1889,15 @@ struct F32FragMN {
     }
 };
 
-// BM x BN tile (256x256 with 2x4 waves of 128x64, or 128x128 with 2x2 waves
-// of 64x64, two blocks per CU), 32-k stages (two in flight), the DMA issued
-// by waves 0-3; the same pipeline as gemm_kernel_dl.
+// BM x BN tile (256x256 with 2x4 waves of 128x64; 256x192 with 4x3 waves of
+// 64x64; 128x128 with 2x2 waves of 64x64, two blocks per CU), 32-k stages
+// (two in flight), the DMA issued by waves 0-3; the same pipeline as
+// gemm_kernel_dl.
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool AMN, bool BMN, bool GLB>
 __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dlf32(GemmArgs p) {
     constexpr int NT = WAVES_M * WAVES_N * 64, NS = 2;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, TM = WM / 32, TN = WN / 32, kG = 4;
-    constexpr int kStageA = BM * 128, kStageB = BN * 128, kStage = kStageA + kStageB;
-    static_assert(NT / 64 >= 4, "four DMA waves");
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
+    static_assert(NT / 64 >= 4 && WM % 32 == 0 && WN % 32 == 0, "four DMA waves, 32x32 blocks");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1900,6 +1907,8 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dlf32(GemmA
     const bool dma_wave = wave < 4;
     using LA = typename std::conditional<AMN, F32LoaderMN<BM, GLB>, F32LoaderK<BM, GLB>>::type;
     using LB = typename std::conditional<BMN, F32LoaderMN<BN, GLB>, F32LoaderK<BN, GLB>>::type;
+    constexpr int kStageA = LA::kStageBytes, kStageB = LB::kStageBytes, kStage = kStageA + kStageB;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
     LA la((const char *)p.a + (tc.offa + m0 * p.sam) * 4, AMN ? p.sak : p.sam, p.M - m0, p.K, wave, lane);
     LB lb((const char *)p.b + (tc.offb + n0 * p.sbn) * 4, BMN ? p.sbk : p.sbn, p.N - n0, p.K, wave, lane);
     constexpr int kLoadsPerStage = LA::kPer + LB::kPer;

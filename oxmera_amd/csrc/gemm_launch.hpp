@@ -27,6 +27,9 @@ enum TileCfg : int {
     kCfgH_256_1W16 = 7,  // as kCfgH_256_1W on 16x16x32 MFMAs (K-major operands; others take
                          // kCfgH_256_1W)
     kCfgF32_64 = 8,    // f32: 64x64 tile, 2x2 waves of 32x32, BK 32 (problems of <= 64 128x128 tiles)
+    kCfgF32_256x192 = 9,  // f32: 256x192 tile, 4x3 waves of 64x64, direct-to-LDS only (K- or
+                          // M/N-contiguous, 16-byte aligned rows): a whole number of rounds where
+                          // 256x256 tiles leave CUs idle (C4: 256 tiles instead of 192)
 };
 
 struct TileShape {
@@ -42,6 +45,13 @@ constexpr int kStripMaxRows = 16;
 // plain store epilogue (no bias, activation or column sums); `args` is
 // validated by the caller.
 hipError_t launch_gemm_strip(const GemmArgs &args, int dtype, hipStream_t stream);
+
+// f32 on 256x256, 256x192 and 128x128 tiles: the direct-to-LDS kernel
+// (gemm_kernel_dlf32) serves K- or M/N-contiguous operands (la, lb: kLdK or
+// kLdMN) whose rows all start 16-byte aligned, unless OXM_GEMM_F32_DMA=0
+// (read at each call) keeps the register-staged kernel.  256x192 tiles exist
+// on this kernel only.
+bool use_f32_dma(const GemmArgs &a, int la, int lb);
 
 // Launch one batched GEMM.  `args` must be fully validated by the caller;
 // tiles_m/tiles_n/group_m/xcd_remap are filled in here.

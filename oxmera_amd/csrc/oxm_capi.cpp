@@ -332,6 +332,21 @@ bool prefer_256_tiles(int64_t M, int64_t N, int64_t batch) {
     return rounds256 < 0.57 * rounds128;
 }
 
+// f32 256x192 tiles (direct-to-LDS kernel only) when their rounds, at 0.75
+// of a 256x256 round each, beat both other tilings by 5 %: C4's 32 batches
+// of 512x768 are 256 such tiles, one round (0.75) against one round of 192
+// 256x256 tiles (1.0) or 768 128x128 tiles (0.86); 4096^3 stays on 256x256
+// tiles (352 of them would take two rounds).
+bool prefer_256x192_tiles(int64_t M, int64_t N, int64_t batch) {
+    const int64_t n256 = ((M + 255) / 256) * ((N + 255) / 256) * batch;
+    const int64_t n192 = ((M + 255) / 256) * ((N + 191) / 192) * batch;
+    const int64_t n128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
+    const double t256 = (double)((n256 + 255) / 256), t192 = 0.75 * (double)((n192 + 255) / 256);
+    double t128 = (double)n128 / 512.0;
+    t128 = 0.57 * (t128 < 0.5 ? 0.5 : t128);
+    return t192 < 0.95 * (t256 < t128 ? t256 : t128);
+}
+
 int env_int(const char *name, int dflt) {
     const char *v = getenv(name);
     return v && *v ? atoi(v) : dflt;
@@ -686,8 +701,10 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
         // take 64x64 tiles: 256^3 runs on 16 CUs instead of 4
         const int64_t n128 = ((Mt + 127) / 128) * ((N + 127) / 128) * batch;
         cfg = big ? oxm::kCfgF32_256 : (n128 <= 64 ? oxm::kCfgF32_64 : oxm::kCfgF32_128);
+        if (cfg != oxm::kCfgF32_64 && prefer_256x192_tiles(Mt, N, batch)) cfg = oxm::kCfgF32_256x192;
         cfg = env_int("OXM_GEMM_CFG_F32", cfg);
-        if (cfg != oxm::kCfgF32_256 && cfg != oxm::kCfgF32_64) cfg = oxm::kCfgF32_128;
+        if (cfg != oxm::kCfgF32_256 && cfg != oxm::kCfgF32_64 && cfg != oxm::kCfgF32_256x192)
+            cfg = oxm::kCfgF32_128;
     } else {
         cfg = big ? oxm::kCfgH_256 : oxm::kCfgH_128;
         forced = env_int("OXM_GEMM_CFG", -1) >= 0;
@@ -703,6 +720,12 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     }
     int ld_a = classify((const char *)g.a, g.sam, g.sak, g.M, K, g.bsa, nbd, es, ts.bm);
     int ld_b = classify((const char *)g.b, g.sbn, g.sbk, N, K, g.bsb, nbd, es, ts.bn);
+    if (cfg == oxm::kCfgF32_256x192 && !oxm::use_f32_dma(g, ld_a, ld_b)) {
+        // 256x192 tiles run on the direct-to-LDS kernel only
+        cfg = oxm::kCfgF32_256;
+        ts = oxm::tile_shape(cfg);
+        ld_b = classify((const char *)g.b, g.sbn, g.sbk, N, K, g.bsb, nbd, es, ts.bn);
+    }
     // The 16x16x32 one-wave kernel in the band where it measured faster than
     // (or level with) the 2x4-wave kernel: interleaved medians, K-major bf16
     // operands, both with the global-load DMA and its short hazard pad --
