@@ -483,12 +483,14 @@ def kernel_name(kind: str) -> str:
     if kind == "bf16":
         return "gemm_kernel_dli16<bf16_t, true> (global_load_lds DMA, 2 stages of 64 k, 4 waves, 16x16x32 MFMA)"
     if kind == "f32":
-        return "gemm_kernel_dlf32<false, true, true> (direct-to-LDS f32: global_load_lds DMA, 2 stages of 32 k, 8 waves)"
+        return ("gemm_kernel_dlf32<256, 256, 2, 4, false, true, true> (direct-to-LDS f32: global_load_lds DMA, "
+                "2 stages of 32 k, 8 waves)")
     if kind == "c2odd":
         return ("gemm_kernel<float,256,256,2,4,Ld::KR,Ld::MNR> (rows 0-4095) + gemm_strip<float> (row 4096); "
                 "time per launch covers both")
     if kind == "c4":
-        return "gemm_kernel<float,128,128,2,2,Ld::K,Ld::MN> (register-staged, 4 waves, 1.5 rounds of tiles)"
+        return ("gemm_kernel_dlf32<256, 192, 4, 3, false, true, true> (direct-to-LDS f32, 256x192 tiles: 256 tiles, "
+                "one round; 12 waves)")
     if kind == "c1":
         return "gemm_kernel<float,64,64,2,2,Ld::K,Ld::MN> (16 tiles on 16 CUs; launch-latency bound)"
     return "gemm_kernel<float,...> (register-staged; tile chosen by the dispatcher)"
