@@ -94,17 +94,26 @@ hipError_t pick_dli(const GemmArgs &a, int la, int lb, hipStream_t s) {
     return launch_dli<T, true, true>(a, s);
 }
 
-// One wave per SIMD on 16x16x32 MFMAs (K-major operands only).
-template <typename T>
+// One wave per SIMD on 16x16x32 MFMAs (AMN / BMN: the operand is M/N-major).
+template <typename T, bool AMN, bool BMN>
 hipError_t launch_dli16(GemmArgs a, hipStream_t s) {
     a.group_m = 4;
     int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n * a.batch;
     dim3 grid((unsigned)ntiles), block(256);
     if (use_global_dma(a))
-        hipLaunchKernelGGL((gemm_kernel_dli16<T, true>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((gemm_kernel_dli16<T, true, 8, 4, 2, AMN, BMN>), grid, block, 0, s, a);
     else
-        hipLaunchKernelGGL((gemm_kernel_dli16<T, false>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((gemm_kernel_dli16<T, false, 8, 4, 2, AMN, BMN>), grid, block, 0, s, a);
     return hipGetLastError();
+}
+
+// The 16x16x32 one-wave kernel for K- or M/N-contiguous operands.
+template <typename T>
+hipError_t pick_dli16(const GemmArgs &a, int la, int lb, hipStream_t s) {
+    if (la == kLdK && lb == kLdK) return launch_dli16<T, false, false>(a, s);
+    if (la == kLdK) return launch_dli16<T, false, true>(a, s);
+    if (lb == kLdK) return launch_dli16<T, true, false>(a, s);
+    return launch_dli16<T, true, true>(a, s);
 }
 
 template <typename T, int BM, int BN, int WM, int WN, Ld LA>

@@ -9,8 +9,8 @@ hipError_t launch_gemm_f16(const GemmArgs &a, int ld_a, int ld_b, int cfg, hipSt
         // K- or M/N-contiguous operands: direct-to-LDS ring
         if (cfg == kCfgH_128) return pick_dl<f16_t, 128, 128, 2, 2, 2, 64, true>(a, ld_a, ld_b, s);
         if (cfg == kCfgH_256_4W) return pick_dl<f16_t, 256, 256, 2, 2, 2, 64>(a, ld_a, ld_b, s);
-        if (cfg == kCfgH_256_1W16 && ld_a == kLdK && ld_b == kLdK) return launch_dli16<f16_t>(a, s);
-        if (cfg == kCfgH_256_1W || cfg == kCfgH_256_1W16) return pick_dli<f16_t>(a, ld_a, ld_b, s);
+        if (cfg == kCfgH_256_1W16) return pick_dli16<f16_t>(a, ld_a, ld_b, s);
+        if (cfg == kCfgH_256_1W) return pick_dli<f16_t>(a, ld_a, ld_b, s);
         return pick_dl<f16_t, 256, 256, 2, 4, 2, 64, true>(a, ld_a, ld_b, s);
     }
     if (cfg == kCfgH_128) return pick_a<f16_t, 128, 128, 2, 2>(a, ld_a, ld_b, s);

@@ -1043,7 +1043,10 @@ constexpr int waitcnt_vm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | (
 // operand's edge read the last valid ones instead -- they feed only outputs
 // past M or N, which are never stored -- and steps past K re-read the last
 // step into a stage that is never consumed.
-template <int ROWS, int NT, bool MN, int BKS, bool GLB = false>
+//
+// SW16 (M/N-major, read by FragReader16MN): within each 64-byte segment the
+// two 32-byte halves are exchanged when bit 3 of the k-row is set.
+template <int ROWS, int NT, bool MN, int BKS, bool GLB = false, bool SW16 = false>
 struct DirectLoader {
     static constexpr int kWaves = NT / 64;
     static constexpr int kBlocks = ROWS * BKS * 2 / 1024;
@@ -1098,7 +1101,8 @@ struct DirectLoader {
                 const int blk = wave + i * kWaves;
                 const int pos = blk * 1024 + lane * 16;
                 const int r = pos / (ROWS * 2), bir = pos % (ROWS * 2);
-                const int mn = (((bir >> 6) ^ (r & 3)) << 5) + ((bir & 63) >> 1);
+                const int w = SW16 ? ((bir & 63) ^ (((r >> 3) & 1) << 5)) : (bir & 63);
+                const int mn = (((bir >> 6) ^ (r & 3)) << 5) + (w >> 1);
                 krow[i] = r;
                 if constexpr (GLB) {
                     // rows_left is a multiple of 8 for an M/N-major 16-bit operand
@@ -1621,8 +1625,45 @@ struct FragReader16 {
     }
 };
 
-// 256x256 tile, 2x2 waves of 128x128, one wave per SIMD, K-major 16-bit
-// operands, 16x16x32 MFMAs (OXM_GEMM_CFG=7).  Against the 32x32x16 kernels a
+// 16x16x32 fragments of an M/N-major 16-bit operand from a BKS = 64 stage of
+// a 256-row tile (DirectLoader SW16 layout: 512-byte k-rows, 64-byte segment
+// s of k-row r stored at s ^ (r % 4), its 32-byte halves exchanged when bit
+// 3 of r is set).  Tile I is mn0 + 16 I .. +15, group g is k 32 g .. +31;
+// lane l supplies column mn0 + 16 I + l % 16 at k 32 g + 8 (l / 16) .. +7,
+// as FragReader16 does for a K-major operand, from two ds_read_b64_tr_b16
+// (in a 16-lane group, lane a + 4 j addresses k-row k0 + j at columns
+// 4 a .. 4 a + 3 of the 16, and lane i receives k0 .. k0 + 3 of column i).
+// A half-wave's accesses (8 k-rows: k0 + j and k0 + 8 + j, 32 bytes each)
+// fall in distinct banks.
+struct FragReader16MN {
+    uint32_t rb[2][2];  // per (g, t): k-row 32 g + 8 (l / 16) + 4 t + j, plus 8 a
+    uint32_t x[8];      // per tile: the segment and half swizzle
+    __device__ __forceinline__ FragReader16MN(uint32_t region, int mn0, int lane) {
+        const int q = lane >> 4, i = lane & 15, a = i & 3, j = i >> 2;
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) rb[g][t] = region + (32 * g + 8 * q + 4 * t + j) * 512 + 8 * a;
+#pragma unroll
+        for (int I = 0; I < 8; ++I) {
+            const int c = (mn0 >> 4) + I;  // 32-byte column chunk of tile I
+            x[I] = (uint32_t)((((c >> 1) ^ j) << 6) | (((c & 1) ^ (q & 1)) << 5));
+        }
+    }
+    template <int I>
+    __device__ __forceinline__ uint4 read1(const uint8_t *stage, int g) const {
+        typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4 *)(uintptr_t)(uint32_t)(uintptr_t)(stage + rb[g][0] + x[I]));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4 *)(uintptr_t)(uint32_t)(uintptr_t)(stage + rb[g][1] + x[I]));
+        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+        return make_uint4(l2.x, l2.y, h2.x, h2.y);
+    }
+};
+
+// 256x256 tile, 2x2 waves of 128x128, one wave per SIMD, 16-bit operands
+// (each K- or, AMN / BMN, M/N-major), 16x16x32 MFMAs (OXM_GEMM_CFG=7).  Against the 32x32x16 kernels a
 // 16x16x32 MFMA is half as long, so each fragment read and DMA instruction
 // of the hand-placed stream has twice as many MFMA slots to hide in: a
 // 64-k stage is two groups of 64 MFMA slots (8 x 8 blocks); slot 2r of a
@@ -1633,7 +1674,7 @@ struct FragReader16 {
 // spacing 1 / 2 / 3, per-wave DMA offsets; this one measured best).  The
 // second group of each stage is deferred past the barrier.  The MFMA sums
 // equal those of the 32x32x16 kernels bit for bit on the shapes tested.
-template <typename T, bool GLB = false, int DF = 8, int DS = 4, int RS = 2>
+template <typename T, bool GLB = false, int DF = 8, int DS = 4, int RS = 2, bool AMN = false, bool BMN = false>
 __global__ void __launch_bounds__(256) gemm_kernel_dli16(GemmArgs p) {
     constexpr int BM = 256, BN = 256, BKS = 64, NT = 256, WAVES_N = 2;
     constexpr int WM = 128, WN = 128, TM = 8, TN = 8;  // 16x16 blocks per wave
@@ -1648,17 +1689,19 @@ __global__ void __launch_bounds__(256) gemm_kernel_dli16(GemmArgs p) {
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const TileCoord tc = tile_coord<BM, BN>(p, blockIdx.x);
     const int64_t m0 = tc.m0, n0 = tc.n0;
-    using LA = DirectLoader<BM, NT, false, BKS, GLB>;
-    using LB = DirectLoader<BN, NT, false, BKS, GLB>;
+    using LA = DirectLoader<BM, NT, AMN, BKS, GLB, AMN>;
+    using LB = DirectLoader<BN, NT, BMN, BKS, GLB, BMN>;
     LA la((const char *)p.a + (tc.offa + m0 * p.sam) * 2, p.sam, p.sak, p.M - m0, p.K, wave, lane);
     LB lb((const char *)p.b + (tc.offb + n0 * p.sbn) * 2, p.sbn, p.sbk, p.N - n0, p.K, wave, lane);
     constexpr int L = LA::kPer + LB::kPer;  // DMA instructions per wave per stage
     constexpr int Q = TM * TN;              // MFMA slots per group
-    constexpr int R = TM + TN;              // fragment reads per group
+    constexpr int R = TM + TN;              // fragment reads per group (two instructions when M/N-major)
     static_assert(DF + (L - 1) * DS < 2 * Q, "DMA must fit the slots of one stage");
     static_assert((R - 1) * RS < Q, "fragment reads must fit the slots of one group");
-    const FragReader16 fra(0, wm * WM, lane);
-    const FragReader16 frb(kStageA, wn * WN, lane);
+    using FA = typename std::conditional<AMN, FragReader16MN, FragReader16>::type;
+    using FB = typename std::conditional<BMN, FragReader16MN, FragReader16>::type;
+    const FA fra(0, wm * WM, lane);
+    const FB frb(kStageA, wn * WN, lane);
 
     f32x4_t acc[TM][TN];
 #pragma unroll

@@ -24,8 +24,7 @@ enum TileCfg : int {
     kCfgF32_256 = 5,   // f32: 256x256 tile, 2x4 waves of 128x64, BK 32 (problems of >= 256 tiles)
     kCfgH_256_1W = 6,  // 16-bit direct-to-LDS 256x256, 2x2 waves of 128x128, one wave per SIMD,
                        // hand-interleaved MFMA / fragment-read / DMA stream
-    kCfgH_256_1W16 = 7,  // as kCfgH_256_1W on 16x16x32 MFMAs (K-major operands; others take
-                         // kCfgH_256_1W)
+    kCfgH_256_1W16 = 7,  // as kCfgH_256_1W on 16x16x32 MFMAs (K- or M/N-contiguous operands)
     kCfgF32_64 = 8,    // f32: 64x64 tile, 2x2 waves of 32x32, BK 32 (problems of <= 64 128x128 tiles)
     kCfgF32_256x192 = 9,  // f32: 256x192 tile, 4x3 waves of 64x64, direct-to-LDS only (K- or
                           // M/N-contiguous, 16-byte aligned rows): a whole number of rounds where

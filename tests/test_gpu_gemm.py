@@ -122,8 +122,9 @@ def test_layouts_full(hip, dtype, la, lb):
 # ragged edge tiles in M and N and a K tail: 1 = 256x256 direct-to-LDS, 2x4
 # waves (the default for large problems); 3 = the same with 2x2 waves; 4 =
 # 256x256 register-staged; 6 = 256x256 direct-to-LDS with one wave per SIMD
-# and a hand-placed instruction stream; 7 = the same on 16x16x32 MFMAs (both
-# operands K-major; other layouts take 6); 2 = 128x128.
+# and a hand-placed instruction stream; 7 = the same on 16x16x32 MFMAs (K- or
+# M/N-major operands: transposing fragment reads for the latter; gathers take
+# 6); 2 = 128x128.
 TILE_CFGS = {"256": 1, "256_4w": 3, "256_regstaged": 4, "256_1w": 6, "256_1w16": 7, "128": 2}
 EDGE_SHAPES = [(300, 200, 264), (264, 136, 520), (64, 72, 64), (520, 64, 8)]
 
