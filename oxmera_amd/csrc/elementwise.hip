@@ -696,6 +696,64 @@ __global__ void __launch_bounds__(256) reduce_cols_vec(RedGeom g, const void *x,
     }
 }
 
+// Columns of a tall input in one pass, no workspace: block b takes the
+// 8 * V consecutive outputs 8 V b .. (eight 16-byte vectors: 128 bytes of a
+// row), thread (j, q) vector j over reduced elements q, q + 64, q + 128, ...
+// (kRedU loads in flight), and the 64 phases of an output are combined in q
+// order through LDS -- a fixed order.  Used when there are enough 128-byte
+// column groups to give every CU a block (the [8192, 8192] f32 column sum:
+// 256 blocks, against 2048 split blocks + a finishing pass before).
+constexpr int kTallPhases = 64;
+
+template <int DT, int OP>
+__global__ void __launch_bounds__(8 * kTallPhases) reduce_cols_tall(RedGeom g, const void *x, void *out) {
+    constexpr int V = DT == kDtF32 ? 4 : 8;
+    __shared__ float part[kTallPhases][8 * V];
+    const int j = threadIdx.x % 8, q = threadIdx.x / 8;
+    const int64_t o = ((int64_t)blockIdx.x * 8 + j) * V;
+    float acc[kRedU][V];
+#pragma unroll
+    for (int u = 0; u < kRedU; ++u)
+#pragma unroll
+        for (int e = 0; e < V; ++e) acc[u][e] = red_identity<OP, float>();
+    if (o < g.n_out) {
+        const int64_t base = dims_offset(g.nk, g.kshape, g.kst, o);
+        for (int64_t r = q; r < g.n_red; r += (int64_t)kTallPhases * kRedU) {
+            float v[kRedU][V];
+#pragma unroll
+            for (int u = 0; u < kRedU; ++u) {
+                const int64_t rr = r + (int64_t)u * kTallPhases;
+                if (rr < g.n_red) {
+                    ld16<DT>(x, base + red_offset(g, rr), v[u]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) v[u][e] = red_identity<OP, float>();
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kRedU; ++u)
+#pragma unroll
+                for (int e = 0; e < V; ++e) acc[u][e] = red_combine<OP, float>(acc[u][e], v[u][e]);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+        float t = acc[0][e];
+#pragma unroll
+        for (int u = 1; u < kRedU; ++u) t = red_combine<OP, float>(t, acc[u][e]);
+        part[q][j * V + e] = t;
+    }
+    __syncthreads();
+    if (threadIdx.x < 8 * V) {
+        const int64_t oo = (int64_t)blockIdx.x * 8 * V + threadIdx.x;
+        if (oo < g.n_out) {
+            float t = part[0][threadIdx.x];
+            for (int k = 1; k < kTallPhases; ++k) t = red_combine<OP, float>(t, part[k][threadIdx.x]);
+            El<DT>::store(out, oo, t);
+        }
+    }
+}
+
 // The finishing pass for the column schedule (ws[s * n_out + o]): 64
 // consecutive outputs per block, four threads per output; thread (o, q)
 // combines splits q, q + 4, q + 8, ... (kRedU loads in flight), then the
@@ -829,7 +887,7 @@ hipError_t ew_dispatch(int nops, int op, const EwShape &s, void *out, const void
 // loads when cols_vec), or a thread per output; splits > 1 combines partial
 // results from a workspace of sizeof(Acc) * n_out * splits bytes.
 struct RedPlan {
-    bool rows, cols, cols_vec;
+    bool rows, cols, cols_vec, cols_tall;
     int64_t splits;
 };
 
@@ -849,7 +907,17 @@ RedPlan plan_reduce(const RedGeom &g, const void *x) {
         for (int d = 0; d + 1 < g.nk; ++d) pl.cols_vec = pl.cols_vec && g.kst[d] % V == 0;
         for (int d = 0; d < g.nr; ++d) pl.cols_vec = pl.cols_vec && g.rst[d] % V == 0;
     }
+    // one pass over 128-byte column groups when they give every CU a block and
+    // each of the 64 row phases a few loads
+    if constexpr (DT != kDtF64) {
+        constexpr int V = DT == kDtF32 ? 4 : 8;
+        pl.cols_tall = pl.cols_vec && g.n_out / (8 * V) >= 256 && g.n_red >= 4 * kTallPhases;
+    }
     int64_t splits = 1;
+    if (pl.cols_tall) {
+        pl.splits = 1;
+        return pl;
+    }
     if (pl.rows) {
         splits = 2048 / g.n_out;  // (8192 blocks for one output measured slower: 0.057 vs 0.051 ms)
         const int64_t cap = g.n_red / 4096;  // >= 4096 elements per block
@@ -881,6 +949,14 @@ hipError_t red_launch(const RedGeom &g, const void *x, void *out, hipStream_t st
     if (!rows && !cols) {
         hipLaunchKernelGGL((reduce_per_thread<DT, OP>), dim3(grid_for(g.n_out)), dim3(256), 0, st, g, x, out);
         return hipGetLastError();
+    }
+    if constexpr (DT != kDtF64) {
+        if (pl.cols_tall) {
+            constexpr int V = DT == kDtF32 ? 4 : 8;
+            hipLaunchKernelGGL((reduce_cols_tall<DT, OP>), dim3((unsigned)((g.n_out + 8 * V - 1) / (8 * V))),
+                               dim3(8 * kTallPhases), 0, st, g, x, out);
+            return hipGetLastError();
+        }
     }
     A *ws = nullptr;
     bool owned = false;

@@ -144,7 +144,9 @@ def test_division_ieee(hip):
 
 REDUCE_CASES = [((64, 48), [0]), ((64, 48), [1]), ((64, 48), []), ((3, 5, 129), [0, 2]), ((3, 5, 129), [1]),
                 ((7, 300, 9), [1]), ((2, 70000), [1]), ((40000, 3), [0]), ((1 << 21,), []),
-                ((3000, 200), [0]), ((300, 1000), [1]), ((9, 40, 3, 100), [0, 2])]
+                ((3000, 200), [0]), ((300, 1000), [1]), ((9, 40, 3, 100), [0, 2]),
+                # one-pass column schedule (at least 256 groups of 128 bytes of outputs)
+                ((300, 16384), [0]), ((3, 260, 8192), [1])]
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=IDS)

@@ -50,9 +50,10 @@ def test_noalloc_reduce_matches_oxm_reduce_twice(hip, dtype):
 
 
 def test_noalloc_reduce_refuses_what_does_not_fit(hip):
-    # bf16 [8192, 16384] column sums: 256 splits x 16384 f32 partials = 16 MiB > 8 MiB
+    # bf16 [8192, 16320] column sums: 255 groups of 64 outputs, one short of
+    # the one-pass schedule, so 256 splits x 16320 f32 partials = 16 MiB > 8 MiB
     print("noalloc refusal", flush=True)
-    x = ox.Tensor.empty((8192, 16384), ox.DType.BF16, DEV)
+    x = ox.Tensor.empty((8192, 16320), ox.DType.BF16, DEV)
     st, _ = run(_lib.lib().oxm_reduce_noalloc, _lib.RED_SUM, x, [0])
     assert st == _lib.E_NOT_IMPLEMENTED
     assert "scratch" in _lib.last_error()
