@@ -615,6 +615,44 @@ __global__ void __launch_bounds__(256) reduce_rows(RedGeom g, const void *x, voi
     }
 }
 
+// Rows, one wave per output (many short rows, 16-byte vectors): wave w of
+// block b reduces row 4 b + w, lane l taking vectors l, l + 64, ... (kRedU
+// in flight), then the 64 lanes combine through cross-lane exchanges in a
+// fixed pattern -- no LDS and no block barrier per row.
+template <int DT, int OP>
+__global__ void __launch_bounds__(256) reduce_rows_wave(RedGeom g, const void *x, void *out) {
+    constexpr int V = DT == kDtF32 ? 4 : 8;
+    const int lane = threadIdx.x & 63;
+    const int64_t o = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (o >= g.n_out) return;  // whole waves leave together
+    const int64_t base = dims_offset(g.nk, g.kshape, g.kst, o);
+    float acc[kRedU];
+#pragma unroll
+    for (int u = 0; u < kRedU; ++u) acc[u] = red_identity<OP, float>();
+    for (int64_t r = (int64_t)lane * V; r < g.n_red; r += 64 * V * kRedU) {
+        float v[kRedU][V];
+#pragma unroll
+        for (int u = 0; u < kRedU; ++u) {
+            if (r + u * 64 * V < g.n_red) {
+                ld16<DT>(x, base + r + u * 64 * V, v[u]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < V; ++e) v[u][e] = red_identity<OP, float>();
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kRedU; ++u)
+#pragma unroll
+            for (int e = 0; e < V; ++e) acc[u] = red_combine<OP, float>(acc[u], v[u][e]);
+    }
+#pragma unroll
+    for (int u = 1; u < kRedU; ++u) acc[0] = red_combine<OP, float>(acc[0], acc[u]);
+    float t = acc[0];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) t = red_combine<OP, float>(t, __shfl_xor(t, off));
+    if (lane == 0) El<DT>::store(out, o, t);
+}
+
 // Columns: consecutive outputs are consecutive in memory (the innermost kept
 // dim has stride 1), so a block of 256 threads takes 256 consecutive outputs
 // (coalesced) over split s of the reduced range, kRedU reduced elements in
@@ -983,6 +1021,11 @@ hipError_t red_launch(const RedGeom &g, const void *x, void *out, hipStream_t st
             constexpr int V = DT == kDtF32 ? 4 : 8;
             vec = (uintptr_t)x % 16 == 0 && g.n_red % V == 0;
             for (int d = 0; d < g.nk; ++d) vec = vec && g.kst[d] % V == 0;
+            if (vec && splits == 1 && g.n_out >= 1024) {
+                hipLaunchKernelGGL((reduce_rows_wave<DT, OP>), dim3((unsigned)((g.n_out + 3) / 4)), dim3(256), 0, st, g,
+                                   x, out);
+                return hipGetLastError();
+            }
             if (vec)
                 hipLaunchKernelGGL((reduce_rows<DT, OP, true>), dim3((unsigned)(g.n_out * splits)), dim3(256), 0, st, g,
                                    x, out, ws, (int)splits);

@@ -146,7 +146,9 @@ REDUCE_CASES = [((64, 48), [0]), ((64, 48), [1]), ((64, 48), []), ((3, 5, 129), 
                 ((7, 300, 9), [1]), ((2, 70000), [1]), ((40000, 3), [0]), ((1 << 21,), []),
                 ((3000, 200), [0]), ((300, 1000), [1]), ((9, 40, 3, 100), [0, 2]),
                 # one-pass column schedule (at least 256 groups of 128 bytes of outputs)
-                ((300, 16384), [0]), ((3, 260, 8192), [1])]
+                ((300, 16384), [0]), ((3, 260, 8192), [1]),
+                # a wave per row (at least 1024 rows of whole 16-byte vectors)
+                ((1100, 264), [1]), ((3, 400, 520), [2])]
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
