@@ -229,6 +229,10 @@ STRIP_CASES = [  # dtype, out dtype, A layout, B layout, M, K, N
     (BF16, BF16, "gather", "col", 2064, 64, 8192),
     (F16, F16, "flip", "row", 2053, 40, 8192),
     (F16, F16, "row", "row", 2065, 40, 8192),
+    # row-major B and K of at least 4 rows per split: the split-K strip
+    (F32, F32, "row", "row", 2050, 300, 8000),
+    (F32, F32, "flip", "row", 2063, 4093, 8188),
+    (BF16, BF16, "row", "row", 2051, 520, 8192),
 ]
 
 
