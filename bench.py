@@ -486,8 +486,8 @@ def kernel_name(kind: str) -> str:
         return ("gemm_kernel_dlf32<256, 256, 2, 4, false, true, true> (direct-to-LDS f32: global_load_lds DMA, "
                 "2 stages of 32 k, 8 waves)")
     if kind == "c2odd":
-        return ("gemm_kernel<float,256,256,2,4,Ld::KR,Ld::MNR> (rows 0-4095) + gemm_strip<float> (row 4096); "
-                "time per launch covers both")
+        return ("gemm_kernel<float,256,256,2,4,Ld::KR,Ld::MNR> (rows 0-4095) + gemm_strip_splitk<float> and "
+                "strip_sum (row 4096); time per launch covers all three")
     if kind == "c4":
         return ("gemm_kernel_dlf32<256, 192, 4, 3, false, true, true> (direct-to-LDS f32, 256x192 tiles: 256 tiles, "
                 "one round; 12 waves)")
