@@ -23,24 +23,24 @@ bool use_global_dma(const GemmArgs &a);
 // a multiple of 32 and OXM_GEMM_GLOBAL_DMA is not 0 (use_f32_dma: gemm_launch.hpp).
 bool use_global_dma_f32(const GemmArgs &a);
 
-template <int BM, int BN, int WM, int WN, bool AMN, bool BMN>
+template <int BM, int BN, int WM, int WN, bool AMN, bool BMN, int NS>
 hipError_t launch_dlf32(GemmArgs a, hipStream_t s) {
     a.group_m = 4;
     int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n * a.batch;
     dim3 grid((unsigned)ntiles), block(WM * WN * 64);
     if (use_global_dma_f32(a))
-        hipLaunchKernelGGL((gemm_kernel_dlf32<BM, BN, WM, WN, AMN, BMN, true>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((gemm_kernel_dlf32<BM, BN, WM, WN, AMN, BMN, true, NS>), grid, block, 0, s, a);
     else
-        hipLaunchKernelGGL((gemm_kernel_dlf32<BM, BN, WM, WN, AMN, BMN, false>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((gemm_kernel_dlf32<BM, BN, WM, WN, AMN, BMN, false, NS>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int NS = 2>
 hipError_t pick_dlf32(const GemmArgs &a, int la, int lb, hipStream_t s) {
-    if (la == kLdK && lb == kLdK) return launch_dlf32<BM, BN, WM, WN, false, false>(a, s);
-    if (la == kLdK) return launch_dlf32<BM, BN, WM, WN, false, true>(a, s);
-    if (lb == kLdK) return launch_dlf32<BM, BN, WM, WN, true, false>(a, s);
-    return launch_dlf32<BM, BN, WM, WN, true, true>(a, s);
+    if (la == kLdK && lb == kLdK) return launch_dlf32<BM, BN, WM, WN, false, false, NS>(a, s);
+    if (la == kLdK) return launch_dlf32<BM, BN, WM, WN, false, true, NS>(a, s);
+    if (lb == kLdK) return launch_dlf32<BM, BN, WM, WN, true, false, NS>(a, s);
+    return launch_dlf32<BM, BN, WM, WN, true, true, NS>(a, s);
 }
 
 // Direct-to-LDS kernel (16-bit operands, each K- or M/N-contiguous).

@@ -1814,9 +1814,9 @@ struct F32LoaderK : DirectLoader<ROWS, 256, false, 64, GLB> {
         : Base(b, 2 * s_mn, 1, rows_left, 2 * k, wave, lane) {}
 };
 
-// M/N-major f32 operand (ROWS = 256, 192 or 128 values along M or N
-// contiguous per k): a k-row of the tile takes 512 bytes of the stage
-// (ROWS = 128) or 1 KB (192 of them used for ROWS = 192), a 1 KB DMA block
+// M/N-major f32 operand (ROWS = 256, 192, 128 or 64 values along M or N
+// contiguous per k): a k-row of the tile takes 4 ROWS bytes of the stage
+// (1 KB, 192 of them used, for ROWS = 192), a 1 KB DMA block
 // holds 1024 / kRowBytes of them; the k-rows whose bit 2 is set are stored
 // rotated by 128 bytes, so a fragment read (lanes 0-31 at k-row k, lanes
 // 32-63 at k + 4, 32 consecutive values each) touches 64 distinct banks.
@@ -1829,9 +1829,9 @@ struct F32LoaderK : DirectLoader<ROWS, 256, false, 64, GLB> {
 // again into a stage nobody reads.
 template <int ROWS, bool GLB>
 struct F32LoaderMN {
-    static_assert(ROWS == 256 || ROWS == 192 || ROWS == 128, "256-, 192- or 128-wide tiles");
+    static_assert(ROWS == 256 || ROWS == 192 || ROWS == 128 || ROWS == 64, "256-, 192-, 128- or 64-wide tiles");
     static constexpr int kWaves = 4;
-    static constexpr int kRowBytes = ROWS == 128 ? 512 : 1024, kRowsPerBlock = 1024 / kRowBytes,
+    static constexpr int kRowBytes = ROWS == 64 ? 256 : (ROWS == 128 ? 512 : 1024), kRowsPerBlock = 1024 / kRowBytes,
                          kLanesPerRow = kRowBytes / 16;
     static constexpr int kStageBytes = 32 * kRowBytes;
     static constexpr int kPer = 32 / kRowsPerBlock / kWaves;  // DMA instructions per wave per stage
@@ -1912,7 +1912,7 @@ struct F32LoaderMN {
 // k = 8 g + 4 (l / 32) + s (s = 0..3), four ds_read_b32 per fragment.
 template <int TILES, int ROWS>
 struct F32FragMN {
-    static constexpr int kRowBytes = ROWS == 128 ? 512 : 1024;
+    static constexpr int kRowBytes = ROWS == 64 ? 256 : (ROWS == 128 ? 512 : 1024);
     uint32_t region;
     int mn0, lane;
     __device__ __forceinline__ F32FragMN(uint32_t r, int m, int l) : region(r), mn0(m), lane(l) {}
@@ -1933,12 +1933,14 @@ struct F32FragMN {
 };
 
 // BM x BN tile (256x256 with 2x4 waves of 128x64; 256x192 with 4x3 waves of
-// 64x64; 128x128 with 2x2 waves of 64x64, two blocks per CU), 32-k stages
-// (two in flight), the DMA issued by waves 0-3; the same pipeline as
-// gemm_kernel_dl.
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool AMN, bool BMN, bool GLB>
+// 64x64; 128x128 with 2x2 waves of 64x64, two blocks per CU; 64x64 with 2x2
+// waves of 32x32), a ring of NS stages of 32 k (NS - 1 in flight while one
+// is consumed: 2 for the large tiles; 8 for 64x64 tiles, whose problems are
+// small enough that the latency of each step, not the MFMAs, sets the
+// time), the DMA issued by waves 0-3; the same pipeline as gemm_kernel_dl.
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool AMN, bool BMN, bool GLB, int NS = 2>
 __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dlf32(GemmArgs p) {
-    constexpr int NT = WAVES_M * WAVES_N * 64, NS = 2;
+    constexpr int NT = WAVES_M * WAVES_N * 64;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, TM = WM / 32, TN = WN / 32, kG = 4;
     static_assert(NT / 64 >= 4 && WM % 32 == 0 && WN % 32 == 0, "four DMA waves, 32x32 blocks");
     const int tid = threadIdx.x;
@@ -1968,17 +1970,39 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dlf32(GemmA
     uint4 fa[2][TM], fb[2][TN];
 
     const int nk = (int)((p.K + 31) / 32);
-    // prologue: stage 0, then (after it landed) stage 1 in flight
-    if (dma_wave) {
-        la.issue(lds, 0, wave);
-        lb.issue(lds + kStageA, 0, wave);
-    }
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    if (dma_wave) {
-        la.issue(lds + kStage, 1, wave);
-        lb.issue(lds + kStage + kStageA, 1, wave);
+    static_assert((NS - 1) * (LA::kPer + LB::kPer) <= 63, "vmcnt counts at most 63 DMA instructions");
+    if constexpr (NS == 2) {
+        // prologue: stage 0, then (after it landed) stage 1 in flight
+        if (dma_wave) {
+            la.issue(lds, 0, wave);
+            lb.issue(lds + kStageA, 0, wave);
+        }
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if (dma_wave) {
+            la.issue(lds + kStage, 1, wave);
+            lb.issue(lds + kStage + kStageA, 1, wave);
+        }
+    } else {
+        // prologue: the first NS stages (those within K) at once, wait for stage 0
+        if (dma_wave) {
+            static_for<0, NS>([&](auto sc) {
+                constexpr int st = decltype(sc)::value;
+                if (st < nk) {
+                    la.issue(lds + st * kStage, st, wave);
+                    lb.issue(lds + st * kStage + kStageA, st, wave);
+                }
+            });
+        }
+        // stage 0 landed: at most (stages issued - 1) x L instructions outstanding
+        static_for<1, NS + 1>([&](auto ic) {
+            constexpr int issued = decltype(ic)::value;
+            if ((nk < NS ? nk : NS) == issued)
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm((issued - 1) * (LA::kPer + LB::kPer)));
+        });
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
     }
     fra.read(lds, 0, fa[0]);
     frb.read(lds, 0, fb[0]);
@@ -1990,6 +2014,10 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dlf32(GemmA
         uint8_t *stage = lds + cur * kStage;
         const typename LA::Stage sta = la.prep(stage, kt + NS);
         const typename LB::Stage stb = lb.prep(stage + kStageA, kt + NS);
+        // DMA instructions that may stay in flight once step kt+1 has landed:
+        // those of the issued steps after it, min(nk - 1, kt + NS - 1) - (kt + 1)
+        const int after = nk - 2 - kt < NS - 2 ? nk - 2 - kt : NS - 2;
+        const int ahead = (after > 0 ? after : 0) * (LA::kPer + LB::kPer);
         static_for<0, kG - 1>([&](auto gc) {
             constexpr int g = decltype(gc)::value;
             fra.read(stage, g + 1, fa[(g + 1) & 1]);
@@ -2009,12 +2037,20 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dlf32(GemmA
             __builtin_amdgcn_sched_barrier(0);
         });
         // every LDS read of step kt landed; this wave's DMA of step kt+1 landed
+        // (NS > 2: the later stages' may still be in flight)
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & ~(0xF << 8));
+        if constexpr (NS == 2) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & ~(0xF << 8));
+        } else {
+            static_for<0, NS - 1>([&](auto ac) {
+                constexpr int a = decltype(ac)::value * (LA::kPer + LB::kPer);
+                if (ahead == a) __builtin_amdgcn_s_waitcnt(waitcnt_vm(a) & ~(0xF << 8));
+            });
+        }
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         constexpr int gl = (kG - 1) & 1;
-        cur ^= 1;
+        cur = cur + 1 == NS ? 0 : cur + 1;
         const uint8_t *next = lds + cur * kStage;
         fra.read(next, 0, fa[0]);
         frb.read(next, 0, fb[0]);
@@ -2022,10 +2058,11 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64) gemm_kernel_dlf32(GemmA
         // the deferred group's MFMAs, the DMA of step kt+2 (into the stage
         // just consumed) spread over them
         constexpr int Q = TM * TN, L = kLoadsPerStage;
+        const bool more = NS == 2 || kt + NS < nk;  // NS > 2: no DMA past K
         static_for<0, Q>([&](auto qc) {
             constexpr int q = decltype(qc)::value;
             Mma<float>::run(acc[q / TN][q % TN], fa[gl][q / TN], fb[gl][q % TN]);
-            if (dma_wave) {
+            if (dma_wave && more) {
                 static_for<q * L / Q, (q + 1) * L / Q>([&](auto lc) {
                     constexpr int l = decltype(lc)::value;
                     if constexpr (l < LA::kPer)

@@ -176,8 +176,10 @@ F32_DMA_SHAPES = [(300, 256, 264), (264, 200, 520), (1000, 1024, 1000), (64, 96,
 
 
 # OXM_GEMM_CFG_F32: 5 = 256x256 tiles, 0 = 128x128 tiles, 9 = 256x192 tiles
-# (direct-to-LDS only: with OXM_GEMM_F32_DMA=0 the host takes 256x256 tiles)
-@pytest.mark.parametrize("cfg", ["5", "0", "9"])
+# (direct-to-LDS only: with OXM_GEMM_F32_DMA=0 the host takes 256x256
+# tiles), 8 = 64x64 tiles (a ring of 8 stages: K of 96-256 fits it, 1024
+# refills it)
+@pytest.mark.parametrize("cfg", ["5", "0", "9", "8"])
 @pytest.mark.parametrize("la,lb", [("row", "row"), ("row", "col"), ("col", "row"), ("col", "col")])
 def test_f32_dma_kernel_matches_register_kernel(hip, monkeypatch, la, lb, cfg):
     monkeypatch.setenv("OXM_GEMM_CFG_F32", cfg)
@@ -196,7 +198,7 @@ def test_f32_dma_kernel_matches_register_kernel(hip, monkeypatch, la, lb, cfg):
         assert_close(ref, O.matmul(a.ora, b.ora), spec_tolerance(F32, k), f"f32 DMA {la}x{lb} {m}x{k}x{n}")
 
 
-@pytest.mark.parametrize("cfg", ["5", "0", "9"])
+@pytest.mark.parametrize("cfg", ["5", "0", "9", "8"])
 def test_f32_dma_kernel_epilogue(hip, monkeypatch, cfg):
     """Bias + GELU with the pre-activation saved, on the f32 direct-to-LDS
     kernel (K a multiple of 32: the global-load DMA)."""
