@@ -492,7 +492,8 @@ def kernel_name(kind: str) -> str:
         return ("gemm_kernel_dlf32<256, 192, 4, 3, false, true, true> (direct-to-LDS f32, 256x192 tiles: 256 tiles, "
                 "one round; 12 waves)")
     if kind == "c1":
-        return "gemm_kernel<float,64,64,2,2,Ld::K,Ld::MN> (16 tiles on 16 CUs; launch-latency bound)"
+        return ("gemm_kernel_dlf32<64, 64, 2, 2, false, true, true, 8> (16 tiles on 16 CUs, all 8 K steps in "
+                "flight; launch-latency bound)")
     return "gemm_kernel<float,...> (register-staged; tile chosen by the dispatcher)"
 
 
