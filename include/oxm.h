@@ -75,11 +75,17 @@ typedef enum {
     OXM_F16 = 7
 } oxm_dtype;
 
-/* Epilogue activation applied in the GEMM's store stage. */
+/* Epilogue activation applied in the GEMM's store stage.  GELU_GRAD and
+ * MUL_AUX are the pair a training step uses: the forward saves GELU'(z) (one
+ * more multiply-add on the normal CDF and density GELU computes anyway) and
+ * the backward multiplies by it, instead of saving z and evaluating GELU'(z)
+ * again in the backward's epilogue. */
 typedef enum {
-    OXM_ACT_NONE = 0,  /* out = acc + bias                                   */
-    OXM_ACT_GELU = 1,  /* aux_out = acc + bias; out = GELU_erf(acc + bias)   */
-    OXM_ACT_DGELU = 2  /* out = acc * GELU_erf'(aux[m,n])  (backward of GELU) */
+    OXM_ACT_NONE = 0,      /* out = acc + bias                                        */
+    OXM_ACT_GELU = 1,      /* aux_out = acc + bias; out = GELU_erf(acc + bias)        */
+    OXM_ACT_DGELU = 2,     /* out = acc * GELU_erf'(aux[m,n])  (backward of GELU)      */
+    OXM_ACT_GELU_GRAD = 3, /* aux_out = GELU_erf'(acc + bias); out = GELU_erf(acc + bias) */
+    OXM_ACT_MUL_AUX = 4    /* out = acc * aux[m,n]  (backward of GELU from GELU_GRAD's aux) */
 } oxm_act;
 
 #define OXM_MAX_DIMS 8
@@ -97,10 +103,11 @@ typedef struct {
     int32_t device;
 } oxm_view;
 
-/* Fused epilogue.  bias: [N] of bias_dtype on the device, or NULL.  aux: a
- * contiguous [batch..., M, N] buffer of out_dtype: written with the
- * pre-activation for OXM_ACT_GELU (may be NULL), read as Z for OXM_ACT_DGELU
- * (required).  out_dtype must equal the dtype of the output view.
+/* Fused epilogue.  bias: [N] of bias_dtype on the device, or NULL (not
+ * applied under DGELU / MUL_AUX).  aux: a contiguous [batch..., M, N] buffer of
+ * out_dtype: written with the pre-activation for OXM_ACT_GELU or with
+ * GELU'(pre-activation) for OXM_ACT_GELU_GRAD (may be NULL), read as Z for
+ * OXM_ACT_DGELU and as the factor for OXM_ACT_MUL_AUX (required).  out_dtype must equal the dtype of the output view.
  * colsum: an F32 [N] device buffer, or NULL; when set, the call overwrites it
  * with the sums over all rows (and batches) of the output AS STORED (after
  * rounding to the output dtype) -- the bias gradient of a Linear layer whose

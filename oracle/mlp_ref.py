@@ -7,10 +7,10 @@ Linear h->d + bias, MSE against a target, W stored [in, out] ("XW").
 
 `step_oracle` composes the oracle GEMM (oracle/oxm_oracle.c) with the same
 rounding points as the GPU path:
-  Z1 = bf16(X.W1 + b1)          H = bf16(GELU(X.W1 + b1))   (GELU of the f32 value)
+  G1 = bf16(GELU'(X.W1 + b1))   H = bf16(GELU(X.W1 + b1))   (both of the f32 value)
   Y  = bf16(H.W2 + b2)          loss = mean((Y - T)^2)      dY = bf16(2 (Y - T) / n)
   dW2 = H^T.dY (f32)            db2 = sum_rows dY (f32)
-  dZ1 = bf16((dY.W2^T) * GELU'(Z1))
+  dZ1 = bf16((dY.W2^T) * G1)
   dW1 = X^T.dZ1 (f32)           db1 = sum_rows dZ1 (f32)    dX = bf16(dZ1.W1^T)
 `step_float64` is the same model in float64 with exact erf (no rounding),
 and `loss_float64` its forward, for finite-difference checks.
@@ -36,7 +36,7 @@ def step_oracle(x, w1, b1, w2, b2, t, nthreads=None):
     """All arguments are bf16 bit arrays (uint16).  Returns a dict of the
     forward/backward results (bf16 results as bits, f32 as float32)."""
     kw = dict(nthreads=nthreads)
-    h, z1 = O.matmul(_view(x), _view(w1), out_dtype=O.BF16, bias=b1, bias_dtype=O.BF16, act=O.ACT_GELU,
+    h, g1 = O.matmul(_view(x), _view(w1), out_dtype=O.BF16, bias=b1, bias_dtype=O.BF16, act=O.ACT_GELU_GRAD,
                      want_aux=True, **kw)
     y = O.matmul(_view(h), _view(w2), out_dtype=O.BF16, bias=b2, bias_dtype=O.BF16, **kw)
     yf, tf = O.bf16_to_f32(y), O.bf16_to_f32(t)
@@ -46,11 +46,11 @@ def step_oracle(x, w1, b1, w2, b2, t, nthreads=None):
     dy = O.bf16_round(d * np.float32(2.0 / n))
     dw2 = O.matmul(_tview(h), _view(dy), out_dtype=O.F32, **kw)
     db2 = O.colsum(dy, O.BF16)
-    dz1 = O.matmul(_view(dy), _tview(w2), out_dtype=O.BF16, act=O.ACT_DGELU, aux=z1, **kw)
+    dz1 = O.matmul(_view(dy), _tview(w2), out_dtype=O.BF16, act=O.ACT_MUL_AUX, aux=g1, **kw)
     dw1 = O.matmul(_tview(x), _view(dz1), out_dtype=O.F32, **kw)
     db1 = O.colsum(dz1, O.BF16)
     dx = O.matmul(_view(dz1), _tview(w1), out_dtype=O.BF16, **kw)
-    return dict(z1=z1, h=h, y=y, loss=loss, dy=dy, dw2=dw2, db2=db2, dz1=dz1, dw1=dw1, db1=db1, dx=dx)
+    return dict(g1=g1, h=h, y=y, loss=loss, dy=dy, dw2=dw2, db2=db2, dz1=dz1, dw1=dw1, db1=db1, dx=dx)
 
 
 def _gelu64(z):
@@ -81,4 +81,5 @@ def step_float64(x, w1, b1, w2, b2, t):
     dw1 = x.T @ dz
     db1 = dz.sum(0)
     dx = dz @ w1.T
-    return dict(z1=z, h=h, y=y, loss=loss, dy=dy, dw2=dw2, db2=db2, dz1=dz, dw1=dw1, db1=db1, dx=dx)
+    return dict(z1=z, g1=_dgelu64(z), h=h, y=y, loss=loss, dy=dy, dw2=dw2, db2=db2, dz1=dz, dw1=dw1, db1=db1,
+                dx=dx)

@@ -23,7 +23,7 @@ HERE = Path(__file__).resolve().parent
 LIB = HERE / "_build" / "liboxm_oracle.so"
 
 F32, F64, BF16, F16 = 0, 1, 6, 7
-ACT_NONE, ACT_GELU, ACT_DGELU = 0, 1, 2
+ACT_NONE, ACT_GELU, ACT_DGELU, ACT_GELU_GRAD, ACT_MUL_AUX = 0, 1, 2, 3, 4
 STATUS = {0: "ok", 1: "ShapeMismatch", 2: "BroadcastIncompatible", 3: "DTypeMismatch", 4: "UnsupportedDType",
           7: "RankMismatch"}
 
@@ -122,8 +122,8 @@ def matmul(a: StridedView, b: StridedView, *, out_dtype: int = F32, bias: np.nda
            rows: np.ndarray | None = None, want_aux: bool = False, nthreads: int | None = None):
     """The reference matmul.  Returns C (f32 array, or uint16 bits for a
     16-bit out_dtype).  ``rows``: flattened (batch*M + m) rows to compute;
-    the result is then [len(rows), N].  With ``want_aux`` (GELU), returns
-    (C, pre_activation)."""
+    the result is then [len(rows), N].  With ``want_aux`` (GELU / GELU_GRAD),
+    returns (C, aux): the pre-activation, or GELU' of it."""
     if len(a.shape) < 2 or len(b.shape) < 2:
         raise OracleError(7)
     shape = out_shape(a, b) if a.shape[-1] == b.shape[-2] else None

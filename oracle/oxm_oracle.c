@@ -22,8 +22,9 @@
  * matmul and no fused epilogue yet, crates/oxmera-core/src/dtype.rs:9-22):
  *   - bf16 / f16 operands are widened exactly to f32;
  *   - accumulation is f32, ascending k;
- *   - epilogue: pre = acc + bias[n]; act NONE / GELU(erf) / DGELU
- *     (acc * GELU'(aux[m,n])); the output is rounded once to its dtype
+ *   - epilogue: pre = acc + bias[n]; act NONE / GELU(erf) (aux = pre) /
+ *     DGELU (acc * GELU'(aux[m,n])) / GELU_GRAD (GELU(pre), aux = GELU'(pre))
+ *     / MUL_AUX (acc * aux[m,n]); outputs are rounded once to their dtype
  *     (round-to-nearest-even for bf16/f16).
  *
  * Pinning: tests/test_oracle.py checks every function here against the A4
@@ -39,7 +40,7 @@
 #include <string.h>
 
 enum { OR_F32 = 0, OR_F64 = 1, OR_I32 = 2, OR_I64 = 3, OR_U8 = 4, OR_BOOL = 5, OR_BF16 = 6, OR_F16 = 7 };
-enum { OR_ACT_NONE = 0, OR_ACT_GELU = 1, OR_ACT_DGELU = 2 };
+enum { OR_ACT_NONE = 0, OR_ACT_GELU = 1, OR_ACT_DGELU = 2, OR_ACT_GELU_GRAD = 3, OR_ACT_MUL_AUX = 4 };
 enum { OR_OK = 0, OR_E_SHAPE = 1, OR_E_BROADCAST = 2, OR_E_DTYPE = 3, OR_E_UNSUPPORTED = 4, OR_E_RANK = 7 };
 
 #define OR_MAXDIM 8
@@ -184,7 +185,7 @@ typedef struct {
     const void *bias;
     int bias_dtype;
     int act;
-    void *aux;               /* GELU: pre-activation out (out_dtype); DGELU: Z input (out_dtype) */
+    void *aux;               /* DGELU: Z input; MUL_AUX: the factor (out_dtype) */
     const int64_t *rows;     /* flattened (batch*M + m) rows to compute, NULL = all */
     int64_t nrows;
     void *out;               /* [nrows, N] (rows given) or the full [batch..., M, N] */
@@ -219,10 +220,15 @@ static void compute_row(const job_t *j, int64_t flat, int64_t out_row) {
         if (j->act == OR_ACT_DGELU) {
             float z = load_f(j->aux, j->out_dtype, flat * j->N + n);
             v = acc * dgelu_f(z);
+        } else if (j->act == OR_ACT_MUL_AUX) {
+            v = acc * load_f(j->aux, j->out_dtype, flat * j->N + n);
         } else {
             if (j->bias) v = acc + load_f(j->bias, j->bias_dtype, n);
             if (j->act == OR_ACT_GELU) {
                 if (j->aux_rows) store_f(j->aux_rows, j->out_dtype, o, v);
+                v = gelu_f(v);
+            } else if (j->act == OR_ACT_GELU_GRAD) {
+                if (j->aux_rows) store_f(j->aux_rows, j->out_dtype, o, dgelu_f(v));
                 v = gelu_f(v);
             }
         }

@@ -17,6 +17,7 @@ from .tensor import Storage, Tensor, bf16_bits_to_f32, f32_to_bf16_bits
 from .backend import HipBackend, backend_for, device_count, init, register_backend
 
 ACT_NONE, ACT_GELU, ACT_DGELU = _lib.ACT_NONE, _lib.ACT_GELU, _lib.ACT_DGELU
+ACT_GELU_GRAD, ACT_MUL_AUX = _lib.ACT_GELU_GRAD, _lib.ACT_MUL_AUX
 
 __all__ = [
     "BackendUnavailable", "BroadcastIncompatible", "Device", "DeviceMismatch", "DivisionByZero", "DType",
@@ -24,5 +25,5 @@ __all__ = [
     "HipError", "IndexOutOfBounds", "InvalidArgument", "Layout", "NotImplementedOp", "OxmError", "RankMismatch",
     "ShapeMismatch", "UnsupportedDType", "broadcast_shapes", "contiguous_strides", "numel", "Storage", "Tensor",
     "bf16_bits_to_f32", "f32_to_bf16_bits", "HipBackend", "backend_for", "device_count", "init",
-    "register_backend", "ACT_NONE", "ACT_GELU", "ACT_DGELU",
+    "register_backend", "ACT_NONE", "ACT_GELU", "ACT_DGELU", "ACT_GELU_GRAD", "ACT_MUL_AUX",
 ]

@@ -33,6 +33,8 @@ E_DIVISION_BY_ZERO = 12
 ACT_NONE = 0
 ACT_GELU = 1
 ACT_DGELU = 2
+ACT_GELU_GRAD = 3  # out = GELU(acc + bias), aux = GELU'(acc + bias)
+ACT_MUL_AUX = 4    # out = acc * aux
 
 UN_NEG, UN_EXP, UN_LN, UN_ABS, UN_SIGN = 0, 1, 2, 3, 4
 BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV, BIN_EQ, BIN_DGELU = 0, 1, 2, 3, 4, 5

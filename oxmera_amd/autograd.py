@@ -10,16 +10,18 @@ rest).  Supported: matmul (batched, broadcast), add / sub / mul / div
 abs, sum, max (ties share the gradient equally), and the two fused nodes
 of the Linear MLP:
 
-  linear    h = act(x.W + b)       one GEMM, bias (+ GELU) fused, pre-activation z kept
+  linear    h = act(x.W + b)       one GEMM, bias (+ GELU) fused; with GELU the same
+                                   epilogue saves GELU'(z) of the pre-activation z
   mse_loss  mean((y - t)^2)        loss and dy in one pass
 
 whose backward emits exactly the MLP's GEMMs:
 
   dW = x^T . dz          A is a transposed VIEW of x (no copy), f32 result
   dx = dz . W^T          B is a transposed VIEW of W; when x is the output of a
-                         GELU layer and that layer's only consumer, GELU'(z) is
-                         fused into this GEMM (x.grad then holds dz, the
-                         gradient w.r.t. that layer's pre-activation)
+                         GELU layer and that layer's only consumer, the
+                         product with the saved GELU'(z) is fused into this
+                         GEMM (x.grad then holds dz, the gradient w.r.t. that
+                         layer's pre-activation)
   db = sums over rows of dz, formed by whichever kernel produces dz (the MSE
                          pass, or the dx GEMM's epilogue) when that kernel's
                          output is dz's only contribution; otherwise one
@@ -382,8 +384,9 @@ def matmul(a, b, out_dtype: DType | None = None) -> Var:
 
 
 class _LinearNode(_Node):
-    def __init__(self, x: Var, w: Var, b: Optional[Var], act: int, z: Optional[Tensor]):
-        self.x, self.w, self.b, self.act, self.z = x, w, b, act, z
+    def __init__(self, x: Var, w: Var, b: Optional[Var], act: int, gd: Optional[Tensor]):
+        # gd: GELU'(z) of the pre-activation z, saved by the forward epilogue
+        self.x, self.w, self.b, self.act, self.gd = x, w, b, act, gd
         self.inputs = (x, w, b)
         self.db: Optional[Tensor] = None  # bias gradient formed by the producer of dz
 
@@ -394,7 +397,7 @@ class _LinearNode(_Node):
         be = ctx.be
         if self.act == _lib.ACT_GELU and not dout_is_preact:
             # the output fed something other than one Linear: dz = dout * GELU'(z)
-            dz = be.dgelu(_as(be, dout, self.z.dtype), self.z)
+            dz = be.mul(_as(be, dout, self.gd.dtype), self.gd)
         else:
             dz = dout  # gradient w.r.t. the pre-activation
         x2 = _rows(self.x.t)
@@ -415,7 +418,7 @@ class _LinearNode(_Node):
             if fuse and prod.wants_db():
                 db_prev = Tensor.empty((self.w.t.shape[0],), DType.F32, dz.device)
             dx = be.matmul(_as(be, dz, self.w.t.dtype), self.w.t.transpose_last(), out_dtype=self.x.t.dtype,
-                           act=_lib.ACT_DGELU if fuse else _lib.ACT_NONE, aux=prod.z if fuse else None,
+                           act=_lib.ACT_MUL_AUX if fuse else _lib.ACT_NONE, aux=prod.gd if fuse else None,
                            colsum=db_prev)
             if db_prev is not None:
                 prod.db = db_prev
@@ -454,11 +457,13 @@ def linear(x: Var, w: Var, b: Optional[Var] = None, act: int = _lib.ACT_NONE) ->
     """y = act(x . w + b) with w stored [in, out] (as "XW" implies)."""
     be = backend_for(x.t.device)
     rg = _rg(x, w, b)
-    keep_z = act == _lib.ACT_GELU and rg
+    # a GELU layer on the tape saves GELU'(z) from the same epilogue
+    keep = act == _lib.ACT_GELU and rg
     out_shape = x.t.shape[:-1] + (w.t.shape[-1],)
-    z = Tensor.empty(out_shape, x.t.dtype, x.t.device) if keep_z else None
-    y = be.matmul(x.t, w.t, out_dtype=x.t.dtype, bias=b.t if b is not None else None, act=act, aux=z)
-    return _record(y, _LinearNode(x, w, b, act, z) if rg else None)
+    gd = Tensor.empty(out_shape, x.t.dtype, x.t.device) if keep else None
+    y = be.matmul(x.t, w.t, out_dtype=x.t.dtype, bias=b.t if b is not None else None,
+                  act=_lib.ACT_GELU_GRAD if keep else act, aux=gd)
+    return _record(y, _LinearNode(x, w, b, act, gd) if rg else None)
 
 
 def mse_loss(y: Var, target: Tensor) -> Var:

@@ -72,7 +72,10 @@ struct Elem<f16_t> {
 };
 
 enum : int { kDtF32 = 0, kDtBF16 = 6, kDtF16 = 7 };
-enum : int { kActNone = 0, kActGelu = 1, kActDGelu = 2 };
+enum : int { kActNone = 0, kActGelu = 1, kActDGelu = 2, kActGeluGrad = 3, kActMulAux = 4 };
+
+// Whether the epilogue reads aux (as Z, or as the factor) rather than writing it.
+__device__ __forceinline__ bool act_reads_aux(int act) { return act == kActDGelu || act == kActMulAux; }
 
 // ---- scalar helpers ------------------------------------------------------
 
@@ -130,6 +133,13 @@ __device__ __forceinline__ float gelu_erf(float x) { return x * normal_parts(x).
 __device__ __forceinline__ float dgelu_erf(float x) {
     const NormalParts n = normal_parts(x);
     return n.cdf + x * n.e * 0.39894228040143267794f;  // 1 / sqrt(2 pi)
+}
+
+// GELU(x) and GELU'(x) from one evaluation of the normal parts.
+__device__ __forceinline__ void gelu_and_grad(float x, float &g, float &d) {
+    const NormalParts n = normal_parts(x);
+    g = x * n.cdf;
+    d = n.cdf + x * n.e * 0.39894228040143267794f;
 }
 
 // ---- LDS layout ----------------------------------------------------------
@@ -586,6 +596,10 @@ __device__ __forceinline__ void store4(const GemmArgs &p, int64_t o, float4 v, b
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             if (i < nvalid) x[i] *= dgelu_erf(z4[i]);
+    } else if (p.act == kActMulAux) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i < nvalid) x[i] *= z4[i];
     } else {
         if (p.bias) {
 #pragma unroll
@@ -597,6 +611,12 @@ __device__ __forceinline__ void store4(const GemmArgs &p, int64_t o, float4 v, b
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 if (i < nvalid) x[i] = gelu_erf(x[i]);
+        } else if (p.act == kActGeluGrad) {
+            float d[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (i < nvalid) gelu_and_grad(x[i], x[i], d[i]);
+            if (p.aux) store4_out<OUT_DT>(p.aux, o, d, vec, nvalid);
         }
     }
     if (p.colsum) {
@@ -664,8 +684,9 @@ __device__ __forceinline__ void unpack4(const uint2 &u, float (&z)[4]) {
 // Writes one 32-row slab of a wave's accumulators (already staged in LDS as
 // f32 [32][WN + 8]) to C with coalesced 4-element stores; lane l owns columns
 // col0 + 4 (l % (WN/4)) .. +3 of rows l / (WN/4), + 64/(WN/4), ...  b4: the
-// bias of the lane's four columns.  PRE: GELU' with the slab's aux values
-// prefetched in `pre` (lanes that could not prefetch load them here).
+// bias of the lane's four columns.  PRE: an aux-reading epilogue (GELU',
+// MUL_AUX) with the slab's aux values prefetched in `pre` (lanes that could
+// not prefetch load them here).
 template <int OUT_DT, int WN, bool PRE>
 __device__ __forceinline__ void write_slab(const GemmArgs &p, const float *ws, int64_t cbase, int64_t row0,
                                            int64_t col0, int lane, const float (&b4)[4], float (&cs)[4],
@@ -702,7 +723,7 @@ __device__ __forceinline__ void write_slab(const GemmArgs &p, const float *ws, i
             if (row >= p.M || nvalid == 0) continue;
             const int64_t o = cbase + row * p.N + col;
             float z4[4] = {0.f, 0.f, 0.f, 0.f};
-            if (p.act == kActDGelu) load4_out<OUT_DT>(p.aux, o, vec, nvalid, z4);
+            if (act_reads_aux(p.act)) load4_out<OUT_DT>(p.aux, o, vec, nvalid, z4);
             const float4 v = *(const float4 *)(ws + r * kSld + c4);
             store4<OUT_DT>(p, o, v, vec, nvalid, b4, z4, cs);
         }
@@ -787,11 +808,11 @@ __device__ __forceinline__ void epilogue_slabs(const GemmArgs &p, Acc (&acc)[TM]
                                                int64_t cbase, int64_t row_base, int64_t col0, const float (&b4)[4],
                                                float (&cs)[4]) {
     constexpr int NSLAB = kSlabs<Acc, TM>;
-    // GELU' with 16-bit output and 64-column wave tiles: every slab's aux
-    // values (64 VGPRs at most) load before the first store; otherwise
-    // write_slab loads them per row
+    // an aux-reading epilogue (GELU', MUL_AUX) with 16-bit output and
+    // 64-column wave tiles: every slab's aux values (64 VGPRs at most) load
+    // before the first store; otherwise write_slab loads them per row
     constexpr bool kPre = OUT_DT != kDtF32 && WN <= 64;
-    const bool pre_ok = kPre && p.act == kActDGelu && slab_aligned(p);
+    const bool pre_ok = kPre && act_reads_aux(p.act) && slab_aligned(p);
     AuxSlab<OUT_DT, WN> pre[kPre ? NSLAB : 1];
     if constexpr (kPre) {
         if (pre_ok) {
@@ -820,7 +841,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmArgs &p, Acc (&acc)[TM][T
     float *ws = (float *)lds + wave * 32 * kSld;
     float cs[4] = {0.f, 0.f, 0.f, 0.f};  // column sums of the stored output (p.colsum)
     float b4[4] = {0.f, 0.f, 0.f, 0.f};  // bias of this lane's four columns (the same in every row)
-    if (p.bias && p.act != kActDGelu) {
+    if (p.bias && !act_reads_aux(p.act)) {
         const int64_t col = col0 + (lane % (WN / 4)) * 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i)

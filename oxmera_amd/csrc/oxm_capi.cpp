@@ -595,10 +595,13 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
                     oxm::kMaxBatchDims);
     oxm_epilogue none = {nullptr, OXM_F32, OXM_ACT_NONE, nullptr, nullptr};
     if (!ep) ep = &none;
-    if (ep->act < OXM_ACT_NONE || ep->act > OXM_ACT_DGELU)
+    if (ep->act < OXM_ACT_NONE || ep->act > OXM_ACT_MUL_AUX)
         return fail(OXM_E_INVALID_ARGUMENT, "matmul: unknown epilogue activation %d", ep->act);
     if (ep->act == OXM_ACT_DGELU && !ep->aux)
         return fail(OXM_E_INVALID_ARGUMENT, "matmul: the DGELU epilogue needs the pre-activation (aux)");
+    if (ep->act == OXM_ACT_MUL_AUX && !ep->aux)
+        return fail(OXM_E_INVALID_ARGUMENT, "matmul: the MUL_AUX epilogue needs its factor (aux)");
+    const bool aux_in = ep->act == OXM_ACT_DGELU || ep->act == OXM_ACT_MUL_AUX;
     if (ep->bias && !is_gemm_dtype(ep->bias_dtype))
         return fail(OXM_E_UNSUPPORTED_DTYPE, "dtype %s is not supported by matmul (bias)", dtype_name(ep->bias_dtype));
 
@@ -637,11 +640,11 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
         const struct {
             Span out;
             const char *name;
-        } outs[3] = {{sc, "output"}, {ep->act == OXM_ACT_DGELU ? Span{0, 0} : saux, "aux output"}, {scs, "colsum"}};
+        } outs[3] = {{sc, "output"}, {aux_in ? Span{0, 0} : saux, "aux output"}, {scs, "colsum"}};
         const struct {
             Span in;
             const char *name;
-        } ins[4] = {{sa, "lhs"}, {sb, "rhs"}, {sbias, "bias"}, {ep->act == OXM_ACT_DGELU ? saux : Span{0, 0}, "aux"}};
+        } ins[4] = {{sa, "lhs"}, {sb, "rhs"}, {sbias, "bias"}, {aux_in ? saux : Span{0, 0}, "aux"}};
         for (const auto &o : outs) {
             for (const auto &i : ins)
                 if ((st = refuse_overlap(o.out, o.name, i.in, i.name, op)) != OXM_OK) return st;

@@ -429,8 +429,13 @@ def test_gelu_accuracy(hip):
     z = ox.Tensor.from_numpy(np.repeat(x.reshape(m, 1), n, axis=1), d)
     dg = hip.matmul(ox.Tensor.from_numpy(np.ones((m, 1), np.float32), d), ones_b, act=ox.ACT_DGELU,
                     aux=z).to_numpy()
+    # GELU_GRAD: GELU of x out, GELU'(x) to aux, from one evaluation
+    gd_aux = ox.Tensor.empty((m, n), F32, d)
+    g2 = hip.matmul(ox.Tensor.from_numpy(x.reshape(m, 1), d), ones_b, act=ox.ACT_GELU_GRAD, aux=gd_aux).to_numpy()
+    assert np.array_equal(g2, g), "GELU_GRAD's output differs from GELU's"
+    dg2 = gd_aux.to_numpy()
     bound = 1e-6 * np.maximum(1.0, np.abs(xd))
-    for got, ref, what in ((g, g_ref, "GELU"), (dg, dg_ref, "GELU'")):
+    for got, ref, what in ((g, g_ref, "GELU"), (dg, dg_ref, "GELU'"), (dg2, dg_ref, "GELU_GRAD aux")):
         err = np.abs(got.astype(np.float64) - ref[:, None])
         worst = int(np.argmax(err.max(axis=1) / bound))
         assert np.all(err <= bound[:, None]), f"{what}({x[worst]}) = {got[worst, 0]} vs {ref[worst]}"
@@ -455,6 +460,61 @@ def test_dgelu_epilogue(hip, monkeypatch, dtype, cfg):
     ref = O.matmul(a.ora, b.ora, out_dtype=odt, act=O.ACT_DGELU, aux=zbuf)
     refw = ref if dtype == F32 else O.bf16_to_f32(ref)
     assert_close(to_f32(c), refw, spec_tolerance(dtype, k), "dgelu")
+
+
+@pytest.mark.parametrize("cfg", EPI_CFGS, ids=["auto", "cfg1", "cfg6", "cfg7"])
+@pytest.mark.parametrize("dtype,out", [(F32, F32), (BF16, BF16), (F16, F16)], ids=["f32", "bf16", "f16"])
+def test_gelu_grad_epilogue(hip, monkeypatch, dtype, out, cfg):
+    """GELU_GRAD: out = GELU(acc + bias), aux = GELU'(acc + bias), both
+    rounded to the output dtype, against the oracle."""
+    _force_cfg(monkeypatch, cfg)
+    rng = np.random.default_rng(23)
+    m, k, n = 130, 192, 200
+    a = contiguous_operand(dtype, rng.normal(0, 1, (m, k)))
+    b = make_operand(dtype, "col", k, n, 24, "b")
+    bias_buf = host_buffer(dtype, rng.normal(0, 0.5, n).astype(np.float32))
+    bias = ox.Tensor.from_numpy(bias_buf, ox.Device.rocm(0), dtype)
+    g = ox.Tensor.empty((m, n), out, ox.Device.rocm(0))
+    c = hip.matmul(a.dev, b.dev, out_dtype=out, bias=bias, act=ox.ACT_GELU_GRAD, aux=g)
+    odt = {F32: O.F32, BF16: O.BF16, F16: O.F16}[out]
+    ref, ref_g = O.matmul(a.ora, b.ora, out_dtype=odt, bias=bias_buf, bias_dtype=odt, act=O.ACT_GELU_GRAD,
+                          want_aux=True)
+    widen = (lambda x: O.bf16_to_f32(x)) if out == BF16 else ((lambda x: x.view(np.float16).astype(np.float32))
+                                                              if out == F16 else (lambda x: x))
+    tol = spec_tolerance(dtype, k) if out == F32 else 1e-2
+    # GELU' is at most 1.13 in magnitude: the pre-activation's tolerance carries over
+    assert_close(to_f32(g), widen(ref_g), 1.13 * tol, "GELU'(pre-activation)")
+    assert_close(to_f32(c), widen(ref), tol, "gelu output")
+
+
+@pytest.mark.parametrize("cfg", EPI_CFGS, ids=["auto", "cfg1", "cfg6", "cfg7"])
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
+def test_mul_aux_epilogue(hip, monkeypatch, dtype, cfg):
+    """MUL_AUX: out = acc * aux (no bias), with the column sums of the stored
+    output, against the oracle."""
+    _force_cfg(monkeypatch, cfg)
+    rng = np.random.default_rng(33)
+    m, k, n = 96, 160, 136
+    a = contiguous_operand(dtype, rng.normal(0, 1, (m, k)))
+    b = make_operand(dtype, "col", k, n, 34, "b")
+    fbuf = host_buffer(dtype, rng.uniform(0, 1.1, m * n).astype(np.float32)).reshape(m, n)
+    f = ox.Tensor.from_numpy(fbuf, ox.Device.rocm(0), dtype)
+    cs = ox.Tensor.empty((n,), F32, ox.Device.rocm(0))
+    c = hip.matmul(a.dev, b.dev, out_dtype=dtype, act=ox.ACT_MUL_AUX, aux=f, colsum=cs)
+    odt = O.F32 if dtype == F32 else O.BF16
+    ref = O.matmul(a.ora, b.ora, out_dtype=odt, act=O.ACT_MUL_AUX, aux=fbuf)
+    refw = ref if dtype == F32 else O.bf16_to_f32(ref)
+    got = to_f32(c)
+    assert_close(got, refw, spec_tolerance(dtype, k), "acc * aux")
+    _check_colsum(cs, got, "MUL_AUX column sums")
+
+
+def test_mul_aux_requires_aux(hip):
+    d = ox.Device.rocm(0)
+    x = ox.Tensor.empty((4, 8), F32, d)
+    y = ox.Tensor.empty((8, 4), F32, d)
+    with pytest.raises(ox.InvalidArgument):
+        hip.matmul(x, y, act=ox.ACT_MUL_AUX)
 
 
 def _check_colsum(cs: ox.Tensor, out: np.ndarray, what: str):

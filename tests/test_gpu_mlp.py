@@ -61,7 +61,7 @@ def intermediates(model, x, t):
     yv = fc2(hv)
     lv = mse_loss(yv, t)
     lv.backward()
-    return dict(z1=hv.node.z, h=hv.t, y=yv.t, loss=lv.t, dy=yv.grad, dw2=fc2.w.grad, db2=fc2.b.grad,
+    return dict(g1=hv.node.gd, h=hv.t, y=yv.t, loss=lv.t, dy=yv.grad, dw2=fc2.w.grad, db2=fc2.b.grad,
                 dz1=hv.grad, dw1=fc1.w.grad, db1=fc1.b.grad, dx=x.grad)
 
 
@@ -71,7 +71,7 @@ def test_mlp_small_end_to_end(hip):
     got = intermediates(model, x, T["t"])
     ref = R.step_oracle(host["x"], host["w1"], host["b1"], host["w2"], host["b2"], host["t"])
     assert abs(float(got["loss"].to_numpy()[0]) - float(ref["loss"])) <= 1e-3 * float(ref["loss"])
-    for k in ("z1", "h", "y", "dy", "dz1", "dx"):
+    for k in ("g1", "h", "y", "dy", "dz1", "dx"):
         assert_close(got[k].to_numpy(), O.bf16_to_f32(ref[k]), TOL, k)
     for k in ("dw1", "dw2", "db1", "db2"):
         assert_close(got[k].to_numpy(), ref[k], TOL, k)
@@ -80,7 +80,7 @@ def test_mlp_small_end_to_end(hip):
 def gemm_checks(got, host, rows_per=6, seed=0):
     """Each GEMM of the step on sampled rows, fed the GPU's own inputs."""
     xb, w1b, w2b = host["x"], host["w1"], host["w2"]
-    hb, z1b, dyb, dz1b = bits(got["h"]), bits(got["z1"]), bits(got["dy"]), bits(got["dz1"])
+    hb, g1b, dyb, dz1b = bits(got["h"]), bits(got["g1"]), bits(got["dy"]), bits(got["dz1"])
     V = lambda b: O.StridedView.contiguous(b, O.BF16)
     VT = lambda b: O.StridedView.contiguous(b, O.BF16).permute([1, 0])
     # the oracle reads K-contiguous copies of the same operands (bit-identical
@@ -89,14 +89,14 @@ def gemm_checks(got, host, rows_per=6, seed=0):
     n = xb.shape[0]
     checks = []
     r = sample_rows(n, rows_per, seed)
-    h_ref, z_ref = F(V(xb), V(w1b), out_dtype=O.BF16, bias=host["b1"], bias_dtype=O.BF16,
-                            act=O.ACT_GELU, rows=r, want_aux=True)
-    checks += [("X.W1 (pre-act)", bits(got["z1"])[r], z_ref, True), ("GELU(X.W1+b1)", hb[r], h_ref, True)]
+    h_ref, g_ref = F(V(xb), V(w1b), out_dtype=O.BF16, bias=host["b1"], bias_dtype=O.BF16,
+                     act=O.ACT_GELU_GRAD, rows=r, want_aux=True)
+    checks += [("GELU'(X.W1+b1)", g1b[r], g_ref, True), ("GELU(X.W1+b1)", hb[r], h_ref, True)]
     y_ref = F(V(hb), V(w2b), out_dtype=O.BF16, bias=host["b2"], bias_dtype=O.BF16, rows=r)
     checks.append(("H.W2+b2", bits(got["y"])[r], y_ref, True))
     rh = sample_rows(hb.shape[1], rows_per, seed + 1)
     checks.append(("H^T.dY", got["dw2"].to_numpy()[rh], F(VT(hb), V(dyb), rows=rh), False))
-    dz_ref = F(V(dyb), VT(w2b), out_dtype=O.BF16, act=O.ACT_DGELU, aux=z1b, rows=r)
+    dz_ref = F(V(dyb), VT(w2b), out_dtype=O.BF16, act=O.ACT_MUL_AUX, aux=g1b, rows=r)
     checks.append(("dY.W2^T * GELU'", dz1b[r], dz_ref, True))
     rx = sample_rows(xb.shape[1], rows_per, seed + 2)
     checks.append(("X^T.dZ1", got["dw1"].to_numpy()[rx], F(VT(xb), V(dz1b), rows=rx), False))

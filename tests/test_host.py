@@ -159,6 +159,9 @@ def test_bad_epilogue_refused():
     a, b, c = host_tensor([2, 3]), host_tensor([3, 2]), host_tensor([2, 2])
     ep = _lib.OxmEpilogue(None, 0, 7, None)
     assert gemm_status(a, b, c, ep) in (_lib.E_INVALID_ARGUMENT, _lib.E_DEVICE_MISMATCH)
+    # MUL_AUX without its factor
+    ep = _lib.OxmEpilogue(None, 0, _lib.ACT_MUL_AUX, None)
+    assert gemm_status(a, b, c, ep) in (_lib.E_INVALID_ARGUMENT, _lib.E_DEVICE_MISMATCH)
 
 
 def test_null_view_is_invalid_argument():

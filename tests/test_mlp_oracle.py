@@ -63,7 +63,7 @@ def test_oracle_step_matches_float64_within_bf16(seed):
     # bf16 storage of activations gives ~2^-8 relative error per rounding; the
     # backward chain compounds a few of them.
     assert abs(got["loss"] - ref["loss"]) <= 2e-2 * ref["loss"]
-    for k in ("z1", "h", "y", "dy", "dz1", "dx"):
+    for k in ("g1", "h", "y", "dy", "dz1", "dx"):
         assert rel_close(O.bf16_to_f32(got[k]), ref[k], 3e-2) <= 1.0, k
     for k in ("dw1", "dw2", "db1", "db2"):
         assert rel_close(got[k], ref[k], 3e-2) <= 1.0, k

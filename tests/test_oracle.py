@@ -233,6 +233,31 @@ def test_dgelu_epilogue_multiplies_by_the_derivative(oracle):
     assert np.allclose(fused, plain * deriv, rtol=2e-6, atol=1e-7)
 
 
+def test_gelu_grad_epilogue_saves_the_derivative(oracle):
+    """GELU_GRAD: the output is GELU of the pre-activation (as the GELU
+    epilogue gives it) and the aux its derivative, against the closed form
+    of the pre-activation the GELU epilogue saves."""
+    g = _load("f32_bias_gelu")
+    a, b = golden_views(oracle, g)
+    c1, pre = oracle.matmul(a, b, bias=g["bias"], act=oracle.ACT_GELU, want_aux=True)
+    c2, deriv = oracle.matmul(a, b, bias=g["bias"], act=oracle.ACT_GELU_GRAD, want_aux=True)
+    assert np.array_equal(c1, c2)
+    zd = pre.astype(np.float64)
+    exact = 0.5 * (1 + erf(zd / np.sqrt(2))) + zd * np.exp(-zd * zd / 2) / np.sqrt(2 * np.pi)
+    assert np.all(np.abs(deriv - exact) <= 1e-6)
+
+
+def test_mul_aux_epilogue_multiplies_elementwise(oracle):
+    rng = np.random.default_rng(12)
+    a = rng.uniform(-1, 1, (6, 8)).astype(np.float32)
+    b = rng.uniform(-1, 1, (8, 5)).astype(np.float32)
+    f = rng.normal(size=(6, 5)).astype(np.float32)
+    plain = mm(oracle, a, b)
+    fused = mm(oracle, a, b, act=oracle.ACT_MUL_AUX, aux=f)
+    # one f32 product of the accumulated sum and the factor, correctly rounded
+    assert np.array_equal(fused, (plain.astype(np.float64) * f).astype(np.float32))
+
+
 # ---- GELU and dtype conversions --------------------------------------------------
 
 def test_gelu_matches_scipy_erf(oracle):
