@@ -74,6 +74,10 @@ pub const OXM_ACT_NONE: oxm_act = 0;
 pub const OXM_ACT_GELU: oxm_act = 1;
 /// out = acc * GELU'(aux).
 pub const OXM_ACT_DGELU: oxm_act = 2;
+/// aux = GELU'(acc + bias); out = GELU(acc + bias).
+pub const OXM_ACT_GELU_GRAD: oxm_act = 3;
+/// out = acc * aux.
+pub const OXM_ACT_MUL_AUX: oxm_act = 4;
 
 /// Unary ops (`oxm_unary_op`).
 pub const OXM_UN_NEG: i32 = 0;
