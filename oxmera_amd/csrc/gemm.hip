@@ -1,6 +1,6 @@
 // gemm.hip -- tile-shape table and dtype dispatch of the GEMM kernels.
-// The instantiations live in one translation unit per dtype
-// (gemm_f32.hip, gemm_bf16.hip, gemm_f16.hip) so they build in parallel.
+// The instantiations live in translation units per dtype (gemm_f32*.hip,
+// gemm_bf16*.hip, gemm_f16*.hip) so they build in parallel.
 #include <cstdlib>
 
 #include "gemm_dispatch.hpp"
