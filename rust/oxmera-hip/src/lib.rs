@@ -13,7 +13,7 @@
 //!   library validates everything before launching, and every failure is a
 //!   typed `oxmera_core::Error` (`check`).
 //!
-//! Seam additions this crate relies on, listed in INTEGRATION.md: the
+//! Seam additions this crate relies on in oxmera-core / oxmera-tensor: the
 //! `Device::Rocm { index }` variant, `DType::BF16` / `DType::F16`, and a
 //! device variant of `Storage` (`DeviceBuffer`, `Storage::from_device_buffer`,
 //! `Storage::device_buffer`).
