@@ -697,6 +697,7 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     g.M = Mt;
 
     int cfg;
+    int cfg_plain = 0;  // f32: the configuration without 256x192 tiles
     bool forced = false;
     const bool big = prefer_256_tiles(Mt, N, batch);
     if (a->dtype == OXM_F32) {
@@ -704,6 +705,7 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
         // take 64x64 tiles: 256^3 runs on 16 CUs instead of 4
         const int64_t n128 = ((Mt + 127) / 128) * ((N + 127) / 128) * batch;
         cfg = big ? oxm::kCfgF32_256 : (n128 <= 64 ? oxm::kCfgF32_64 : oxm::kCfgF32_128);
+        cfg_plain = cfg;
         if (cfg != oxm::kCfgF32_64 && prefer_256x192_tiles(Mt, N, batch)) cfg = oxm::kCfgF32_256x192;
         cfg = env_int("OXM_GEMM_CFG_F32", cfg);
         if (cfg != oxm::kCfgF32_256 && cfg != oxm::kCfgF32_64 && cfg != oxm::kCfgF32_256x192)
@@ -724,9 +726,10 @@ oxm_status oxm_gemm(const oxm_view *a, const oxm_view *b, const oxm_view *c, con
     int ld_a = classify((const char *)g.a, g.sam, g.sak, g.M, K, g.bsa, nbd, es, ts.bm);
     int ld_b = classify((const char *)g.b, g.sbn, g.sbk, N, K, g.bsb, nbd, es, ts.bn);
     if (cfg == oxm::kCfgF32_256x192 && !oxm::use_f32_dma(g, ld_a, ld_b)) {
-        // 256x192 tiles run on the direct-to-LDS kernel only
-        cfg = oxm::kCfgF32_256;
+        // 256x192 tiles run on the direct-to-LDS kernel only: the choice without them
+        cfg = cfg_plain;
         ts = oxm::tile_shape(cfg);
+        ld_a = classify((const char *)g.a, g.sam, g.sak, g.M, K, g.bsa, nbd, es, ts.bm);
         ld_b = classify((const char *)g.b, g.sbn, g.sbk, N, K, g.bsb, nbd, es, ts.bn);
     }
     // The 16x16x32 one-wave kernel in the band where it measured faster than

@@ -677,6 +677,20 @@ def test_c3_f16_8192_nt(hip):
     check_checksums(c, a, b, n, "C3 f16")
 
 
+def test_256x192_shape_with_ragged_rows(hip):
+    """C4's shape makes the dispatcher prefer 256x192 tiles, which only the
+    direct-to-LDS kernel has; with rows of 67 floats (not 16-byte aligned)
+    it takes the register-staged kernel on the tiles it would use without
+    256x192 (128x128 here)."""
+    rng = np.random.default_rng(44)
+    log("256x192-preferred shape with ragged A rows")
+    a = contiguous_operand(F32, rng.uniform(-1, 1, (32, 512, 67)))
+    b = contiguous_operand(F32, rng.uniform(-1, 1, (1, 67, 768)))
+    c = hip.matmul(a.dev, b.dev)
+    assert c.shape == (32, 512, 768)
+    check_rows(c, a, b, sample_rows(32 * 512, 256, 45), F32, 67, "ragged 256x192 fallback")
+
+
 def test_c4_batched_broadcast(hip):
     rng = np.random.default_rng(4)
     log("C4 batched broadcast")
